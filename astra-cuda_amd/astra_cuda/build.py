@@ -1,0 +1,58 @@
+"""Builds ``libastra_market.so`` (the HIP engine + C ABI) in-tree for gfx950.
+
+Usage: ``python astra-cuda_amd/astra_cuda/build.py`` or ``astra_cuda.build.build()``.
+The library links the HIP runtime by its SONAME (libamdhip64.so.7); imported after
+torch, it binds to the runtime torch already loaded, so both share streams.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(PKG_DIR))
+CSRC = os.path.join(os.path.dirname(PKG_DIR), "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+LIB_NAME = "libastra_market.so"
+LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+
+ARCH = os.environ.get("ASTRA_OFFLOAD_ARCH", "gfx950")
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-mcode-object-version=5",
+    # keep the compiler from emitting packed FP32 ops (unused here anyway)
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found; the HIP engine cannot be built")
+
+
+def build(verbose: bool = False) -> str:
+    """Compile csrc/market.hip into the package directory. Always recompiles."""
+    src = os.path.join(CSRC, "market.hip")
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", src, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

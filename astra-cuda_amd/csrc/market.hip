@@ -1,0 +1,967 @@
+// market.hip -- MI355X (gfx950) VecMarket order-matching engine behind the C ABI
+// declared in include/astra_market.h.
+//
+// Semantics follow the reference kernels of nlyu1/astra-cuda
+// src/order_matching/market.cu (add_orders_kernel :17-100, match_orders_kernel
+// :102-278, get_bbo_kernel :280-320, update_last_prices_kernel :767-786) bit for
+// bit, including what ring-slot reuse does to the level lists (a reused slot is
+// never unlinked, so stale heads, cut chains, self links and zero/negative-size
+// fills happen exactly as in the reference). The data layout and the kernels are
+// this engine's own:
+//
+//  * One lane per market. A market's matching is a serial dependency chain
+//    (each fill decides the next pair of heads), so the 64 lanes of a wavefront
+//    carry 64 independent markets and the memory system sees M independent
+//    chains at once.
+//  * Per market and side, the occupancy of the L price levels is a bitmask of
+//    W = ceil(L/64) 64-bit words kept in registers during a call; bit p is set
+//    exactly when the level's head is not NULL. Best bid / best ask are
+//    count-leading/trailing-zeros over the mask, replacing the reference's
+//    O(L) rescans. The masks live in HBM as structure-of-arrays
+//    mask[side][word][market], so their loads and stores are fully coalesced.
+//  * Level lists are packed: level p of market m is 8 bytes
+//    {bid_head, bid_tail, ask_head, ask_tail} as uint16 (NULL = 0xFFFF), so one
+//    32-bit access reads or writes a side's head and tail together and the
+//    levels around the mid share a few 128-byte lines.
+//  * An order slot is one 16-byte record {size, customer, tid, price | next<<16},
+//    read with a single 128-bit load. order_is_bid is not stored: nothing in the
+//    reference ever reads it (written at market.cu:54,83 only).
+//  * Portfolio updates are fire-and-forget atomic adds (no return value), so
+//    they stay off the matching chain. int32 wrap-around is the same as the
+//    reference's plain += / -=.
+//
+// Behaviour the reference leaves undefined (out-of-bounds indexing) is defined
+// here and in the CPU oracle in the same way: negative prices are not inserted,
+// negative customer ids do not touch portfolios. Every slot index read from the
+// book is bounds-checked before it is dereferenced.
+//
+// Every kernel body is a __host__ __device__ function behind a thin __global__
+// wrapper. Built with -DASTRA_HOST_EMULATION (host-only compile), the same
+// bodies run in plain loops over host memory behind the same C ABI; the tests
+// use that build to check the logic and its bounds on the CPU.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "astra_market.h"
+
+#define ASTRA_HD __host__ __device__ __forceinline__
+
+namespace {
+
+constexpr uint32_t kNull16 = 0xFFFFu;
+constexpr int kFillThreads = 256;
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+
+// Mirrors ASTRA_CHECK_OP's text (src/utils/astra_utils.h:116-131).
+#define ASTRA_ABI_CHECK(x_exp, op, y_exp)                                               \
+  do {                                                                                  \
+    long long x_ = (long long)(x_exp), y_ = (long long)(y_exp);                         \
+    if (!(x_ op y_))                                                                    \
+      return fail(ASTRA_ERR_INVALID_ARGUMENT,                                           \
+                  std::string("market.hip:") + std::to_string(__LINE__) + " " #x_exp    \
+                      " " #op " " #y_exp "\n" #x_exp " = " + std::to_string(x_) +       \
+                      ", " #y_exp " = " + std::to_string(y_));                          \
+  } while (false)
+
+#define ASTRA_HIP_CHECK(call, what)                                                     \
+  do {                                                                                  \
+    hipError_t e_ = (call);                                                             \
+    if (e_ != hipSuccess)                                                               \
+      return fail(ASTRA_ERR_HIP, std::string("HIP error in ") + (what) + ": " +         \
+                                     hipGetErrorString(e_));                           \
+  } while (false)
+
+// ---- runtime shims: the device build calls HIP, the emulation build works on
+// host memory ----
+#ifdef ASTRA_HOST_EMULATION
+hipError_t rt_device_count(int *n) {
+  *n = 1;
+  return hipSuccess;
+}
+hipError_t rt_memcpy(void *d, const void *s, size_t n, hipStream_t) {
+  std::memmove(d, s, n);
+  return hipSuccess;
+}
+hipError_t rt_sync(hipStream_t) { return hipSuccess; }
+hipError_t rt_last_error() { return hipSuccess; }
+struct DeviceGuard {
+  bool ok = true;
+  explicit DeviceGuard(int) {}
+};
+void rt_device_sync(int) {}
+#else
+hipError_t rt_device_count(int *n) { return hipGetDeviceCount(n); }
+hipError_t rt_memcpy(void *d, const void *s, size_t n, hipStream_t st) {
+  return hipMemcpyAsync(d, s, n, hipMemcpyDefault, st);
+}
+hipError_t rt_sync(hipStream_t st) { return hipStreamSynchronize(st); }
+hipError_t rt_last_error() { return hipGetLastError(); }
+// Restores the calling thread's current device when it goes out of scope.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = true;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+void rt_device_sync(int dev) {
+  DeviceGuard g(dev);
+  (void)hipDeviceSynchronize();
+}
+#endif
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+inline int mask_words_for(int32_t L) {
+  const int w = (L + 63) / 64;
+  if (w <= 1) return 1;
+  if (w <= 2) return 2;
+  if (w <= 4) return 4;
+  if (w <= 8) return 8;
+  return 16;
+}
+
+// Byte offsets of the book arrays inside the workspace.
+struct Layout {
+  int W;
+  size_t masks, next_slot, levels, records, portfolios, total;
+};
+
+Layout make_layout(int64_t M, int64_t L, int64_t O, int64_t C) {
+  Layout l;
+  l.W = mask_words_for((int32_t)L);
+  size_t off = 0;
+  l.masks = off;
+  off = align_up(off + (size_t)2 * l.W * M * 8, 256);
+  l.next_slot = off;
+  off = align_up(off + (size_t)M * 4, 256);
+  l.levels = off;
+  off = align_up(off + (size_t)M * L * 8, 256);
+  l.records = off;
+  off = align_up(off + (size_t)M * O * 16, 256);
+  l.portfolios = off;
+  off = align_up(off + (size_t)M * C * 8, 256);
+  l.total = off;
+  return l;
+}
+
+}  // namespace
+
+struct astra_market {
+  int32_t M, L, O, F, C;
+  int device;
+  int32_t threads_per_block;  // validated, not used for launches
+  int32_t flags;
+  int32_t tid;                // host TID counter, market.h:338
+  int block;                  // launch block size of the per-market kernels
+  unsigned long long *stats;  // see astra_market_set_stats
+  char *ws;
+  size_t ws_bytes;
+  Layout lay;
+};
+
+namespace {
+
+struct Book {
+  uint64_t *masks;            // [2][W][M]: side 0 = bid, 1 = ask
+  int32_t *next_slot;         // [M], in [0, O)
+  uint16_t *levels;           // [M][L][4] = {bid_head, bid_tail, ask_head, ask_tail}
+  uint4 *records;             // [M][O] = {size, customer, tid, price | next << 16}
+  int32_t *portfolios;        // [M][C][2] = {contracts, cash}
+  unsigned long long *stats;  // diagnostic counters [4] or nullptr
+  int32_t M, L, O, F, C;
+};
+
+Book book_of(const astra_market *h) {
+  Book b;
+  b.masks = reinterpret_cast<uint64_t *>(h->ws + h->lay.masks);
+  b.next_slot = reinterpret_cast<int32_t *>(h->ws + h->lay.next_slot);
+  b.levels = reinterpret_cast<uint16_t *>(h->ws + h->lay.levels);
+  b.records = reinterpret_cast<uint4 *>(h->ws + h->lay.records);
+  b.portfolios = reinterpret_cast<int32_t *>(h->ws + h->lay.portfolios);
+  b.stats = h->stats;
+  b.M = h->M;
+  b.L = h->L;
+  b.O = h->O;
+  b.F = h->F;
+  b.C = h->C;
+  return b;
+}
+
+struct QuoteIn {
+  const int32_t *bid_px, *bid_sz, *ask_px, *ask_sz, *cust;
+  int32_t base_tid;
+};
+
+struct FillOut {
+  int32_t *prices, *sizes, *taker, *quoter;
+  uint8_t *is_sell_quote;
+  int32_t *quote_sizes, *tid, *quote_tid, *counts;
+};
+
+// ---- small device/host helpers ----
+
+ASTRA_HD int clz64(uint64_t x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __clzll(x);
+#else
+  return x ? __builtin_clzll(x) : 64;
+#endif
+}
+
+ASTRA_HD int ctz64(uint64_t x) {  // x != 0
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __ffsll((unsigned long long)x) - 1;
+#else
+  return __builtin_ctzll(x);
+#endif
+}
+
+// Fire-and-forget add with int32 wrap-around.
+ASTRA_HD void add_i32(int32_t *p, int32_t v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  atomicAdd(p, v);
+#else
+  *p = (int32_t)((uint32_t)*p + (uint32_t)v);
+#endif
+}
+
+ASTRA_HD void add_u64(unsigned long long *p, unsigned long long v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  atomicAdd(p, v);
+#else
+  *p += v;
+#endif
+}
+
+ASTRA_HD int32_t wsub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
+
+// ---- occupancy-mask helpers (W words, fully unrolled, no dynamic indexing) ----
+
+template <int W>
+ASTRA_HD int mask_highest(const uint64_t (&m)[W]) {
+  int r = -1;
+#pragma unroll
+  for (int i = 0; i < W; ++i)
+    if (m[i]) r = i * 64 + 63 - clz64(m[i]);
+  return r;
+}
+
+template <int W>
+ASTRA_HD int mask_lowest(const uint64_t (&m)[W], int none) {
+  int r = none;
+#pragma unroll
+  for (int i = W - 1; i >= 0; --i)
+    if (m[i]) r = i * 64 + ctz64(m[i]);
+  return r;
+}
+
+// Bit updates are arithmetic per word (no branch selects the word), so the
+// compiler keeps the mask in registers instead of forming an indexed array.
+template <int W>
+ASTRA_HD void mask_set(uint64_t (&m)[W], int p) {
+#pragma unroll
+  for (int i = 0; i < W; ++i) m[i] |= (uint64_t)((p >> 6) == i) << (p & 63);
+}
+
+template <int W>
+ASTRA_HD void mask_clear(uint64_t (&m)[W], int p) {
+#pragma unroll
+  for (int i = 0; i < W; ++i) m[i] &= ~((uint64_t)((p >> 6) == i) << (p & 63));
+}
+
+// Appends one order to the tail of its level list (market.cu:44-70 for the bid,
+// :73-99 for the ask). `word` is the side's {head, tail} pair read before any
+// store of this call; `side` is 0 (bid) or 1 (ask).
+template <int W>
+ASTRA_HD void insert_order(uint16_t *lv, uint4 *rec, uint64_t (&mask)[W], int32_t &ns, int32_t O,
+                           int side, int32_t price, int32_t size, int32_t cust, int32_t tid,
+                           uint32_t word) {
+  const int32_t slot = ns;
+  ns = (ns + 1 == O) ? 0 : ns + 1;
+  rec[slot] = make_uint4((uint32_t)size, (uint32_t)cust, (uint32_t)tid,
+                         (uint32_t)price | (kNull16 << 16));
+  const uint32_t old_tail = word >> 16;
+  uint16_t *pair = lv + (size_t)price * 4 + 2 * side;
+  if (old_tail == kNull16) {
+    *reinterpret_cast<uint32_t *>(pair) = (uint32_t)slot | ((uint32_t)slot << 16);
+    mask_set<W>(mask, price);
+  } else {
+    pair[1] = (uint16_t)slot;
+    if (old_tail < (uint32_t)O) reinterpret_cast<uint16_t *>(rec + old_tail)[7] = (uint16_t)slot;
+  }
+}
+
+// add_orders_kernel + match_orders_kernel (market.cu:17-100, 102-278) for
+// market m. STATS builds the diagnostic variant that also counts inserts, fill
+// rows, emptied levels and overflowed markets.
+template <int W, bool STATS>
+ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut &out, int64_t m) {
+  const int64_t M = b.M;
+  const int32_t L = b.L, O = b.O, F = b.F, C = b.C;
+
+  const int32_t bid_px = in.bid_px[m], bid_sz = in.bid_sz[m];
+  const int32_t ask_px = in.ask_px[m], ask_sz = in.ask_sz[m];
+  const int32_t cust = in.cust[m];
+  uint64_t bm[W], am[W];
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    bm[i] = b.masks[(int64_t)i * M + m];
+    am[i] = b.masks[(int64_t)(W + i) * M + m];
+  }
+  int32_t ns = b.next_slot[m];
+  uint16_t *lv = b.levels + m * (int64_t)L * 4;
+  uint4 *rec = b.records + m * (int64_t)O;
+  int32_t *pf = b.portfolios + m * (int64_t)C * 2;
+
+  // ---- add: bid first, then ask (TIDs base, base + 1) ----
+  const bool bid_ok = bid_sz > 0 && (uint32_t)bid_px < (uint32_t)L;
+  const bool ask_ok = ask_sz > 0 && (uint32_t)ask_px < (uint32_t)L;
+  // Both {head, tail} words are read up front: the bid insert only writes bid
+  // halves of level words, so the ask word it would have read is unchanged.
+  const uint32_t bword = bid_ok ? *reinterpret_cast<const uint32_t *>(lv + (size_t)bid_px * 4) : 0u;
+  const uint32_t aword =
+      ask_ok ? *reinterpret_cast<const uint32_t *>(lv + (size_t)ask_px * 4 + 2) : 0u;
+  if (bid_ok) insert_order<W>(lv, rec, bm, ns, O, 0, bid_px, bid_sz, cust, in.base_tid, bword);
+  if (ask_ok)
+    insert_order<W>(lv, rec, am, ns, O, 1, ask_px, ask_sz, cust,
+                    (int32_t)((uint32_t)in.base_tid + 1u), aword);
+
+  // ---- match while the book is crossed (market.cu:145-274) ----
+  int bb = mask_highest<W>(bm);
+  int ba = mask_lowest<W>(am, L);
+  int32_t fc = 0;
+  uint32_t emptied = 0;
+  int bhl = -1, ahl = -1;                         // level whose head slot is in bsl / asl
+  uint32_t bsl = kNull16, asl = kNull16;          // head slots of the best levels
+  uint32_t brs = 0xFFFFFFFFu, ars = 0xFFFFFFFFu;  // slots whose records are in brec / arec
+  uint4 brec = make_uint4(0, 0, 0, 0), arec = make_uint4(0, 0, 0, 0);
+
+  while (bb >= 0 && ba < L && bb >= ba) {
+    if (bhl != bb) {
+      bsl = lv[(size_t)bb * 4 + 0];
+      bhl = bb;
+    }
+    if (ahl != ba) {
+      asl = lv[(size_t)ba * 4 + 2];
+      ahl = ba;
+    }
+    if (bsl >= (uint32_t)O || asl >= (uint32_t)O) break;  // NULL head (:155)
+    // A record is (re)loaded when its side's head slot changes. Every size
+    // change is written through to the record right away, so memory always
+    // holds the latest size, also for a slot cached on the other side.
+    if (brs != bsl) {
+      brec = rec[bsl];
+      brs = bsl;
+    }
+    if (ars != asl) {
+      arec = rec[asl];
+      ars = asl;
+    }
+    const int32_t bsz = (int32_t)brec.x, asz = (int32_t)arec.x;
+    const int32_t bcu = (int32_t)brec.y, acu = (int32_t)arec.y;
+    const int32_t btid = (int32_t)brec.z, atid = (int32_t)arec.z;
+    const bool bid_quote = btid < atid;  // earlier TID rests (:172)
+    const int32_t price = (int32_t)((bid_quote ? brec.w : arec.w) & kNull16);
+    const int32_t qty = bsz < asz ? bsz : asz;
+    if (fc >= F) {  // overflow sentinel (:187-195)
+      fc = -1;
+      break;
+    }
+    const int64_t fi = m * (int64_t)F + fc;
+    out.prices[fi] = price;
+    out.sizes[fi] = qty;
+    out.taker[fi] = bid_quote ? acu : bcu;
+    out.quoter[fi] = bid_quote ? bcu : acu;
+    out.is_sell_quote[fi] = bid_quote ? 0 : 1;
+    out.quote_sizes[fi] = bid_quote ? bsz : asz;
+    out.tid[fi] = bid_quote ? atid : btid;
+    out.quote_tid[fi] = bid_quote ? btid : atid;
+    // (:221-232) A self-trade nets to zero, so it is skipped.
+    if ((uint32_t)bcu < (uint32_t)C && (uint32_t)acu < (uint32_t)C && bcu != acu) {
+      const uint32_t notional = (uint32_t)price * (uint32_t)qty;
+      add_i32(pf + 2 * bcu, qty);
+      add_i32(pf + 2 * bcu + 1, (int32_t)(0u - notional));
+      add_i32(pf + 2 * acu, (int32_t)(0u - (uint32_t)qty));
+      add_i32(pf + 2 * acu + 1, (int32_t)notional);
+    }
+    ++fc;
+    // (:237-238) both decrements land on one slot when bid and ask alias
+    if (bsl == asl) {
+      const int32_t s = wsub(wsub(bsz, qty), qty);
+      brec.x = arec.x = (uint32_t)s;
+      reinterpret_cast<int32_t *>(rec + bsl)[0] = s;
+    } else {
+      brec.x = (uint32_t)wsub(bsz, qty);
+      arec.x = (uint32_t)wsub(asz, qty);
+      reinterpret_cast<int32_t *>(rec + bsl)[0] = (int32_t)brec.x;
+      reinterpret_cast<int32_t *>(rec + asl)[0] = (int32_t)arec.x;
+    }
+    if (brec.x == 0u) {  // pop the bid head (:241-256)
+      const uint32_t nh = brec.w >> 16;
+      if (nh == kNull16) {
+        *reinterpret_cast<uint32_t *>(lv + (size_t)bb * 4) = 0xFFFFFFFFu;
+        mask_clear<W>(bm, bb);
+        if (STATS) ++emptied;
+        bb = mask_highest<W>(bm);
+        bhl = -1;
+      } else {
+        lv[(size_t)bb * 4] = (uint16_t)nh;
+        bsl = nh;
+      }
+    }
+    if (arec.x == 0u) {  // pop the ask head (:258-273)
+      const uint32_t nh = arec.w >> 16;
+      if (nh == kNull16) {
+        *reinterpret_cast<uint32_t *>(lv + (size_t)ba * 4 + 2) = 0xFFFFFFFFu;
+        mask_clear<W>(am, ba);
+        if (STATS) ++emptied;
+        ba = mask_lowest<W>(am, L);
+        ahl = -1;
+      } else {
+        lv[(size_t)ba * 4 + 2] = (uint16_t)nh;
+        asl = nh;
+      }
+    }
+  }
+
+  out.counts[m] = fc;
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    b.masks[(int64_t)i * M + m] = bm[i];
+    b.masks[(int64_t)(W + i) * M + m] = am[i];
+  }
+  b.next_slot[m] = ns;
+  if (STATS) {  // uniform addresses: the compiler aggregates these per wave
+    add_u64(b.stats + 0, (unsigned long long)(bid_ok + ask_ok));
+    add_u64(b.stats + 1, (unsigned long long)(fc < 0 ? F : fc));
+    add_u64(b.stats + 2, (unsigned long long)emptied);
+    add_u64(b.stats + 3, (unsigned long long)(fc < 0));
+  }
+}
+
+// get_bbo_kernel (market.cu:280-320) for market m: best level from the masks,
+// size of that level's head order; an empty side is (NULL, 0).
+template <int W>
+ASTRA_HD void bbo_market(const Book &b, int32_t *bid_px, int32_t *bid_sz, int32_t *ask_px,
+                         int32_t *ask_sz, int64_t m) {
+  const int64_t M = b.M;
+  uint64_t bm[W], am[W];
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    bm[i] = b.masks[(int64_t)i * M + m];
+    am[i] = b.masks[(int64_t)(W + i) * M + m];
+  }
+  const uint16_t *lv = b.levels + m * (int64_t)b.L * 4;
+  const uint4 *rec = b.records + m * (int64_t)b.O;
+  const int bb = mask_highest<W>(bm);
+  const int ba = mask_lowest<W>(am, b.L);
+  int32_t obp = ASTRA_NULL_INDEX, obs = 0, oap = ASTRA_NULL_INDEX, oas = 0;
+  if (bb >= 0) {
+    const uint32_t h = lv[(size_t)bb * 4];
+    if (h < (uint32_t)b.O) {
+      obp = bb;
+      obs = reinterpret_cast<const int32_t *>(rec + h)[0];
+    }
+  }
+  if (ba < b.L) {
+    const uint32_t h = lv[(size_t)ba * 4 + 2];
+    if (h < (uint32_t)b.O) {
+      oap = ba;
+      oas = reinterpret_cast<const int32_t *>(rec + h)[0];
+    }
+  }
+  bid_px[m] = obp;
+  bid_sz[m] = obs;
+  ask_px[m] = oap;
+  ask_sz[m] = oas;
+}
+
+// update_last_prices_kernel (market.cu:767-786). A count above F (only possible
+// for caller-made fill_counts) leaves the last price unchanged.
+ASTRA_HD void last_price_market(int32_t *last, const int32_t *counts, const int32_t *prices,
+                                int32_t F, int64_t m) {
+  const int32_t c = counts[m];
+  if (c > 0 && c <= F) last[m] = prices[m * (int64_t)F + (c - 1)];
+}
+
+// ClearQuotes (market.cu:735-749) for thread t = (market, level): the level's
+// 8-byte word to all-NULL; the level-0 thread also zeroes the masks and the slot
+// counter. The reference also writes NULL into order_next; here a slot's next is
+// overwritten whenever the slot is reused, and after the clear no list can
+// reach a slot that was not reused, so it is left alone (no observable
+// difference).
+template <int W>
+ASTRA_HD void clear_quotes_thread(const Book &b, const uint8_t *reset, int64_t t) {
+  const int64_t per = b.L > 0 ? b.L : 1;
+  const int64_t m = t / per;
+  const int64_t p = t - m * per;
+  if (m >= b.M || !reset[m]) return;
+  const int64_t M = b.M;
+  if (p < b.L) reinterpret_cast<uint64_t *>(b.levels)[m * (int64_t)b.L + p] = ~0ull;
+  if (p == 0) {
+#pragma unroll
+    for (int i = 0; i < 2 * W; ++i) b.masks[(int64_t)i * M + m] = 0ull;
+    b.next_slot[m] = 0;
+  }
+}
+
+// ---- __global__ wrappers ----
+
+template <int W, bool STATS>
+__global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, FillOut out) {
+  const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (m < b.M) quote_match_market<W, STATS>(b, in, out, m);
+}
+
+template <int W>
+__global__ __launch_bounds__(256) void bbo_kernel(Book b, int32_t *bid_px, int32_t *bid_sz,
+                                                   int32_t *ask_px, int32_t *ask_sz) {
+  const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (m < b.M) bbo_market<W>(b, bid_px, bid_sz, ask_px, ask_sz, m);
+}
+
+__global__ __launch_bounds__(256) void last_price_kernel(int32_t *last, const int32_t *counts,
+                                                         const int32_t *prices, int32_t M,
+                                                         int32_t F) {
+  const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (m < M) last_price_market(last, counts, prices, F, m);
+}
+
+template <int W>
+__global__ __launch_bounds__(256) void clear_quotes_kernel(Book b, const uint8_t *reset,
+                                                           int64_t n) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n) clear_quotes_thread<W>(b, reset, t);
+}
+
+// Grid-stride fill of n 32-bit words; 16-byte stores when dst is 16-byte aligned.
+__global__ __launch_bounds__(kFillThreads) void fill_u32_kernel(uint32_t *dst, int64_t n,
+                                                                uint32_t v, int vec) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n4 = vec ? n / 4 : 0;
+  uint4 *d4 = reinterpret_cast<uint4 *>(dst);
+  const uint4 v4 = make_uint4(v, v, v, v);
+  for (int64_t i = t; i < n4; i += stride) d4[i] = v4;
+  for (int64_t i = n4 * 4 + t; i < n; i += stride) dst[i] = v;
+}
+
+// ---- launchers (kernel on the device build, host loop on the emulation build) ----
+
+hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline unsigned grid_for(int64_t n, int block) { return (unsigned)((n + block - 1) / block); }
+
+template <int W>
+int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &fo,
+                       hipStream_t s) {
+  const Book b = book_of(h);
+#ifdef ASTRA_HOST_EMULATION
+  (void)s;
+  for (int64_t m = 0; m < b.M; ++m) {
+    if (b.stats)
+      quote_match_market<W, true>(b, in, fo, m);
+    else
+      quote_match_market<W, false>(b, in, fo, m);
+  }
+#else
+  if (b.stats)
+    hipLaunchKernelGGL((quote_match_kernel<W, true>), dim3(grid_for(b.M, h->block)),
+                       dim3(h->block), 0, s, b, in, fo);
+  else
+    hipLaunchKernelGGL((quote_match_kernel<W, false>), dim3(grid_for(b.M, h->block)),
+                       dim3(h->block), 0, s, b, in, fo);
+#endif
+  ASTRA_HIP_CHECK(rt_last_error(), "AddTwoSidedQuotes");
+  return ASTRA_OK;
+}
+
+template <int W>
+int launch_bbo(const astra_market *h, int32_t *bp, int32_t *bs, int32_t *ap, int32_t *as,
+               hipStream_t s) {
+  const Book b = book_of(h);
+#ifdef ASTRA_HOST_EMULATION
+  (void)s;
+  for (int64_t m = 0; m < b.M; ++m) bbo_market<W>(b, bp, bs, ap, as, m);
+#else
+  hipLaunchKernelGGL((bbo_kernel<W>), dim3(grid_for(b.M, h->block)), dim3(h->block), 0, s, b,
+                     bp, bs, ap, as);
+#endif
+  ASTRA_HIP_CHECK(rt_last_error(), "GetBBOs");
+  return ASTRA_OK;
+}
+
+template <int W>
+int launch_clear_quotes(const astra_market *h, const uint8_t *reset, hipStream_t s) {
+  const Book b = book_of(h);
+  const int64_t n = (int64_t)std::max<int32_t>(h->L, 1) * h->M;
+#ifdef ASTRA_HOST_EMULATION
+  (void)s;
+  for (int64_t t = 0; t < n; ++t) clear_quotes_thread<W>(b, reset, t);
+#else
+  hipLaunchKernelGGL((clear_quotes_kernel<W>), dim3(grid_for(n, 256)), dim3(256), 0, s, b, reset,
+                     n);
+#endif
+  ASTRA_HIP_CHECK(rt_last_error(), "ClearQuotes");
+  return ASTRA_OK;
+}
+
+#define ASTRA_DISPATCH_W(W_, FN, ...)  \
+  switch (W_) {                        \
+    case 1: return FN<1>(__VA_ARGS__); \
+    case 2: return FN<2>(__VA_ARGS__); \
+    case 4: return FN<4>(__VA_ARGS__); \
+    case 8: return FN<8>(__VA_ARGS__); \
+    default: return FN<16>(__VA_ARGS__); \
+  }
+
+int launch_fill(void *dst, int64_t n_words, uint32_t v, hipStream_t s, const char *what) {
+  if (n_words <= 0) return ASTRA_OK;
+#ifdef ASTRA_HOST_EMULATION
+  (void)s;
+  uint32_t *d = static_cast<uint32_t *>(dst);
+  for (int64_t i = 0; i < n_words; ++i) d[i] = v;
+#else
+  const int vec = reinterpret_cast<uintptr_t>(dst) % 16 == 0;
+  int64_t blocks = ((vec ? n_words / 4 : n_words) + kFillThreads - 1) / kFillThreads;
+  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, 8192));
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(kFillThreads), 0, s,
+                     static_cast<uint32_t *>(dst), n_words, v, vec);
+#endif
+  ASTRA_HIP_CHECK(rt_last_error(), what);
+  return ASTRA_OK;
+}
+
+int launch_last_price(int32_t *last, const int32_t *counts, const int32_t *prices, int32_t M,
+                      int32_t F, hipStream_t s) {
+#ifdef ASTRA_HOST_EMULATION
+  (void)s;
+  for (int64_t m = 0; m < M; ++m) last_price_market(last, counts, prices, F, m);
+#else
+  hipLaunchKernelGGL(last_price_kernel, dim3(grid_for(M, 256)), dim3(256), 0, s, last, counts,
+                     prices, M, F);
+#endif
+  ASTRA_HIP_CHECK(rt_last_error(), "UpdateLastPrices");
+  return ASTRA_OK;
+}
+
+// Empty book: masks 0, slot counters 0, level words NULL, portfolios 0 (the
+// order records are left alone: no list reaches a slot before it is written).
+int init_book(astra_market *h, hipStream_t s) {
+  const Layout &l = h->lay;
+  int rc;
+  if ((rc = launch_fill(h->ws + l.masks, (int64_t)(l.levels - l.masks) / 4, 0u, s, "init")))
+    return rc;
+  if ((rc = launch_fill(h->ws + l.levels, (int64_t)h->M * h->L * 2, 0xFFFFFFFFu, s, "init")))
+    return rc;
+  return launch_fill(h->ws + l.portfolios, (int64_t)h->M * h->C * 2, 0u, s, "init");
+}
+
+int validate_shape(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, int32_t flags) {
+  const bool ext = (flags & ASTRA_FLAG_EXTENDED_SHAPES) != 0;
+  ASTRA_ABI_CHECK(M, >=, 0);
+  ASTRA_ABI_CHECK(L, >=, 0);
+  ASTRA_ABI_CHECK(O, >=, 1);
+  ASTRA_ABI_CHECK(F, >=, 0);
+  ASTRA_ABI_CHECK(C, >=, 0);
+  ASTRA_ABI_CHECK(M, <=, ASTRA_MAX_MARKETS);
+  if (!ext) {  // market.cu:338-342
+    ASTRA_ABI_CHECK(L, <=, ASTRA_PRICE_LEVELS);
+    ASTRA_ABI_CHECK(O, <=, ASTRA_MAX_ACTIVE_ORDERS_PER_MARKET);
+    ASTRA_ABI_CHECK(F, <=, ASTRA_MAX_ACTIVE_FILLS_PER_MARKET);
+    ASTRA_ABI_CHECK(C, <=, ASTRA_MAX_CUSTOMERS);
+  } else {
+    ASTRA_ABI_CHECK(L, <=, ASTRA_EXT_MAX_PRICE_LEVELS);
+    ASTRA_ABI_CHECK(O, <=, ASTRA_EXT_MAX_ORDERS);
+    ASTRA_ABI_CHECK(F, <=, ASTRA_EXT_MAX_FILLS);
+    ASTRA_ABI_CHECK(C, <=, ASTRA_EXT_MAX_CUSTOMERS);
+  }
+  return ASTRA_OK;
+}
+
+int default_block() {
+  const char *e = std::getenv("ASTRA_MARKET_BLOCK");
+  if (e) {
+    const int v = std::atoi(e);
+    if (v == 64 || v == 128 || v == 192 || v == 256) return v;
+  }
+  return 128;
+}
+
+struct Row {
+  int32_t price, size, customer, tid;
+};
+
+// Walks one level's list from its head collecting orders with size > 0
+// (market.cu:628-642). At most O nodes are visited: the reference loops forever
+// on a self-linked slot, which this build does not reproduce.
+void walk_level(const std::vector<uint4> &rec, uint32_t head, int32_t price, int32_t O,
+                std::vector<Row> &rows) {
+  uint32_t slot = head;
+  for (int32_t visited = 0; slot < (uint32_t)O && visited < O; ++visited) {
+    const uint4 r = rec[slot];
+    if ((int32_t)r.x > 0) rows.push_back({price, (int32_t)r.x, (int32_t)r.y, (int32_t)r.z});
+    slot = r.w >> 16;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *astra_last_error(void) { return g_last_error.c_str(); }
+
+int astra_market_workspace_size(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C,
+                                int32_t flags, size_t *bytes) {
+  const int rc = validate_shape(M, L, O, F, C, flags);
+  if (rc) return rc;
+  if (!bytes) return fail(ASTRA_ERR_INVALID_ARGUMENT, "bytes must not be NULL");
+  *bytes = make_layout(M, L, O, C).total;
+  return ASTRA_OK;
+}
+
+int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, int device_id,
+                        int32_t threads_per_block, int32_t flags, void *workspace,
+                        size_t workspace_bytes, void *stream, astra_market **out) {
+  if (!out) return fail(ASTRA_ERR_INVALID_ARGUMENT, "out must not be NULL");
+  *out = nullptr;
+  int rc = validate_shape(M, L, O, F, C, flags);
+  if (rc) return rc;
+  ASTRA_ABI_CHECK(threads_per_block, >, 0);  // market.cu:343-344
+  ASTRA_ABI_CHECK(threads_per_block, <=, 1024);
+  int device_count = 0;
+  ASTRA_HIP_CHECK(rt_device_count(&device_count), "hipGetDeviceCount");
+  ASTRA_ABI_CHECK(device_id, >=, 0);  // market.cu:349-350
+  ASTRA_ABI_CHECK(device_id, <, device_count);
+  const Layout lay = make_layout(M, L, O, C);
+  if (!workspace && lay.total > 0) return fail(ASTRA_ERR_INVALID_ARGUMENT, "workspace is NULL");
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return fail(ASTRA_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  ASTRA_ABI_CHECK(workspace_bytes, >=, lay.total);
+  DeviceGuard g(device_id);
+  if (!g.ok) return fail(ASTRA_ERR_HIP, "hipSetDevice failed");
+  astra_market *h = new astra_market();
+  h->M = M;
+  h->L = L;
+  h->O = O;
+  h->F = F;
+  h->C = C;
+  h->device = device_id;
+  h->threads_per_block = threads_per_block;
+  h->flags = flags;
+  h->tid = 0;
+  h->block = default_block();
+  h->stats = nullptr;
+  h->ws = static_cast<char *>(workspace);
+  h->ws_bytes = workspace_bytes;
+  h->lay = lay;
+  rc = init_book(h, as_stream(stream));
+  // zero the order records once so a fresh workspace holds no garbage
+  if (!rc) rc = launch_fill(h->ws + lay.records, (int64_t)M * O * 4, 0u, as_stream(stream), "init");
+  if (rc) {
+    delete h;
+    return rc;
+  }
+  *out = h;
+  return ASTRA_OK;
+}
+
+int astra_market_destroy(astra_market *h) {
+  if (!h) return ASTRA_OK;
+  rt_device_sync(h->device);  // market.cu:416-417
+  delete h;
+  return ASTRA_OK;
+}
+
+int astra_market_clone(const astra_market *src, void *dst_ws, size_t dst_bytes, void *stream,
+                       astra_market **out) {
+  if (!src || !out) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  *out = nullptr;
+  ASTRA_ABI_CHECK(dst_bytes, >=, src->lay.total);
+  if (!dst_ws && src->lay.total > 0) return fail(ASTRA_ERR_INVALID_ARGUMENT, "workspace is NULL");
+  if (reinterpret_cast<uintptr_t>(dst_ws) % 256 != 0)
+    return fail(ASTRA_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  DeviceGuard g(src->device);
+  if (src->lay.total > 0)
+    ASTRA_HIP_CHECK(rt_memcpy(dst_ws, src->ws, src->lay.total, as_stream(stream)), "clone");
+  astra_market *h = new astra_market(*src);
+  h->stats = nullptr;
+  h->ws = static_cast<char *>(dst_ws);
+  h->ws_bytes = dst_bytes;
+  *out = h;
+  return ASTRA_OK;
+}
+
+int astra_market_add_two_sided_quotes(astra_market *h, const int32_t *bid_px,
+                                      const int32_t *bid_sz, const int32_t *ask_px,
+                                      const int32_t *ask_sz, const int32_t *customer_ids,
+                                      int32_t *fill_prices, int32_t *fill_sizes,
+                                      int32_t *fill_customer_ids, int32_t *fill_quoter_ids,
+                                      uint8_t *fill_is_sell_quote, int32_t *fill_quote_sizes,
+                                      int32_t *fill_tid, int32_t *fill_quote_tid,
+                                      int32_t *fill_counts, void *stream) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  if (h->M > 0) {
+    if (!bid_px || !bid_sz || !ask_px || !ask_sz || !customer_ids || !fill_counts)
+      return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL input or fill_counts pointer");
+    if (h->F > 0 && (!fill_prices || !fill_sizes || !fill_customer_ids || !fill_quoter_ids ||
+                     !fill_is_sell_quote || !fill_quote_sizes || !fill_tid || !fill_quote_tid))
+      return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL fill pointer");
+    DeviceGuard g(h->device);
+    const QuoteIn in{bid_px, bid_sz, ask_px, ask_sz, customer_ids, h->tid};
+    const FillOut fo{fill_prices,        fill_sizes,       fill_customer_ids, fill_quoter_ids,
+                     fill_is_sell_quote, fill_quote_sizes, fill_tid,          fill_quote_tid,
+                     fill_counts};
+    const int rc = [&]() -> int {
+      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match, h, in, fo, as_stream(stream));
+    }();
+    if (rc) return rc;
+  }
+  h->tid = (int32_t)((uint32_t)h->tid + 2u);  // market.cu:531
+  return ASTRA_OK;
+}
+
+int astra_market_get_bbos(const astra_market *h, int32_t *bid_px, int32_t *bid_sz,
+                          int32_t *ask_px, int32_t *ask_sz, void *stream) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  if (h->M == 0) return ASTRA_OK;
+  if (!bid_px || !bid_sz || !ask_px || !ask_sz)
+    return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL BBO pointer");
+  DeviceGuard g(h->device);
+  ASTRA_DISPATCH_W(h->lay.W, launch_bbo, h, bid_px, bid_sz, ask_px, ask_sz, as_stream(stream));
+}
+
+int astra_update_last_prices(int32_t *last, const int32_t *counts, const int32_t *prices,
+                             int32_t M, int32_t F, void *stream) {
+  ASTRA_ABI_CHECK(M, >=, 0);
+  ASTRA_ABI_CHECK(F, >=, 0);
+  if (M == 0) return ASTRA_OK;
+  if (!last || !counts || (F > 0 && !prices))
+    return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL pointer");
+  return launch_last_price(last, counts, prices, M, F, as_stream(stream));
+}
+
+int astra_fill_i32(int32_t *dst, int64_t count, int32_t value, void *stream) {
+  ASTRA_ABI_CHECK(count, >=, 0);
+  if (count == 0) return ASTRA_OK;
+  if (!dst) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL pointer");
+  return launch_fill(dst, count, (uint32_t)value, as_stream(stream), "fill");
+}
+
+int astra_market_reset(astra_market *h, void *stream) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  DeviceGuard g(h->device);
+  const int rc = init_book(h, as_stream(stream));  // market.cu:699-712
+  if (rc) return rc;
+  h->tid = 0;  // market.cu:715
+  return ASTRA_OK;
+}
+
+int astra_market_clear_quotes(astra_market *h, const uint8_t *reset, void *stream) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  if (h->M == 0) return ASTRA_OK;
+  if (!reset) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL reset mask");
+  DeviceGuard g(h->device);
+  ASTRA_DISPATCH_W(h->lay.W, launch_clear_quotes, h, reset, as_stream(stream));
+}
+
+int astra_market_portfolios(const astra_market *h, int32_t **p) {
+  if (!h || !p) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL argument");
+  *p = reinterpret_cast<int32_t *>(h->ws + h->lay.portfolios);
+  return ASTRA_OK;
+}
+
+int astra_market_to_string(const astra_market *h, int32_t market_id, char *buf, size_t buflen,
+                           size_t *needed, void *stream) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  std::string s;
+  char line[160];
+  if (market_id >= h->M || market_id < 0) {  // market.cu:602-604
+    std::snprintf(line, sizeof line, "Error: Invalid market_id %d (num_markets = %d)", market_id,
+                  h->M);
+    s = line;
+  } else {
+    DeviceGuard g(h->device);
+    std::vector<uint16_t> lv((size_t)h->L * 4);
+    std::vector<uint4> rec((size_t)h->O);
+    hipStream_t st = as_stream(stream);
+    if (h->L > 0)
+      ASTRA_HIP_CHECK(rt_memcpy(lv.data(), h->ws + h->lay.levels + (size_t)market_id * h->L * 8,
+                                (size_t)h->L * 8, st),
+                      "ToString");
+    ASTRA_HIP_CHECK(rt_memcpy(rec.data(), h->ws + h->lay.records + (size_t)market_id * h->O * 16,
+                              (size_t)h->O * 16, st),
+                    "ToString");
+    ASTRA_HIP_CHECK(rt_sync(st), "ToString");
+    std::vector<Row> sells, buys;
+    for (int32_t p = 0; p < h->L; ++p) walk_level(rec, lv[(size_t)p * 4 + 2], p, h->O, sells);
+    std::sort(sells.begin(), sells.end(), [](const Row &a, const Row &b) {  // :645-651
+      if (a.price != b.price) return a.price > b.price;
+      return a.tid < b.tid;
+    });
+    for (int32_t p = h->L - 1; p >= 0; --p) walk_level(rec, lv[(size_t)p * 4], p, h->O, buys);
+    std::snprintf(line, sizeof line, "####### %zu sell orders #######\n", sells.size());  // :677
+    s += line;
+    for (const Row &r : sells) {
+      std::snprintf(line, sizeof line, "px %d @ sz %d   id=%d @ t=%d\n", r.price, r.size,
+                    r.customer, r.tid);
+      s += line;
+    }
+    s += "#############################\n";
+    std::snprintf(line, sizeof line, "####### %zu buy orders #######\n", buys.size());
+    s += line;
+    for (const Row &r : buys) {
+      std::snprintf(line, sizeof line, "px %d @ sz %d   id=%d @ t=%d\n", r.price, r.size,
+                    r.customer, r.tid);
+      s += line;
+    }
+    s += "#############################";
+  }
+  if (needed) *needed = s.size();
+  if (buf && buflen > 0) {
+    const size_t k = std::min(buflen - 1, s.size());
+    std::memcpy(buf, s.data(), k);
+    buf[k] = '\0';
+  }
+  return ASTRA_OK;
+}
+
+int astra_market_set_stats(astra_market *h, int64_t *counters) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  if (reinterpret_cast<uintptr_t>(counters) % 8 != 0)
+    return fail(ASTRA_ERR_INVALID_ARGUMENT, "counters must be 8-byte aligned");
+  h->stats = reinterpret_cast<unsigned long long *>(counters);
+  return ASTRA_OK;
+}
+
+int astra_market_get_tid(const astra_market *h, int32_t *tid) {
+  if (!h || !tid) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL argument");
+  *tid = h->tid;
+  return ASTRA_OK;
+}
+
+int astra_market_set_tid(astra_market *h, int32_t tid) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  h->tid = tid;
+  return ASTRA_OK;
+}
+
+}  // extern "C"

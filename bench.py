@@ -1,0 +1,282 @@
+#!/usr/bin/env python3
+"""VecMarket benchmark on one MI355X: quote-matches/s, market-steps/s, p50 step latency.
+
+A *step* is one ``add_two_sided_quotes`` over all markets (plus ``get_bbos`` when
+the config asks for it every step), i.e. one lock-step batch of two-sided quotes
+through the hot path. Inputs are generated on the host by the deterministic
+counter-based generator (astra_cuda.workloads), uploaded, and resident in HBM
+before timing starts.
+
+Phases (only A is the headline; B-D replay the same steps from clones of the
+pre-timed state, so they see exactly the same work):
+  A  throughput: W warm-up steps, then exactly K steps, no host sync inside,
+     bracketed by torch.cuda.synchronize() on both sides;
+  B  latency: per-step host time with the stream synced (p50 / p99 / max);
+  C  device time: HIP events around every kernel launch (stream busy, async);
+  D  work counts: the diagnostic kernel variant counts inserts, fill rows and
+     emptied levels, for the algorithmic-byte roofline.
+Then the CPU baseline: the oracle (a C port of the reference algorithm) on a
+bounded subset of the same markets and steps, all host threads and 1 thread.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "astra-cuda_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+
+
+def log(msg: str) -> None:
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=900, help="timed steps K")
+    ap.add_argument("--warmup", type=int, default=100, help="untimed warm-up steps W")
+    ap.add_argument("--config", type=int, default=3, help="BASELINE.json config index (2, 3 or 4)")
+    ap.add_argument("--markets", type=int, default=0, help="override the config's market count")
+    ap.add_argument("--no-bbo", action="store_true", help="do not call get_bbos every step")
+    ap.add_argument("--latency-steps", type=int, default=300)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU time of the all-thread oracle leg")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of known size (for rocprof counter scaling)")
+    return ap.parse_args()
+
+
+def cpu_info():
+    model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return model, avail
+
+
+def copy_calibration():
+    import torch
+    n = 1 << 30  # 1 GiB
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 10}))
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        msg = ("bench.py measures one GPU only: markets are independent and shard with no "
+               "communication, so N GPUs would run N independent engines; --gpus must be 1")
+        print(msg, file=sys.stderr)
+        sys.exit(2)
+    if args.copy_calibration:
+        return copy_calibration()
+
+    import numpy as np
+    import torch
+    from astra_cuda import order_matching as aom
+    from astra_cuda.workloads import CONFIGS, QuoteStream
+
+    cfg = CONFIGS[args.config]
+    M = args.markets or cfg.M
+    W, K = args.warmup, args.steps
+    T = W + K
+    bbo = cfg.bbo_every_step and not args.no_bbo
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    # ---- inputs: generated on the host, resident in HBM before timing ----
+    t0 = time.perf_counter()
+    qs = QuoteStream(cfg, np.arange(M))
+    host = qs.steps(0, T)
+    log(f"generated config {cfg.index} inputs: {T} steps x {M} markets in {time.perf_counter() - t0:.1f}s")
+    dev_in = [torch.from_numpy(a).to(dev) for a in host]
+    rows = [tuple(x[t] for x in dev_in) for t in range(T)]
+    torch.cuda.synchronize()
+
+    shape = dict(num_markets=M, max_price_levels=cfg.L, max_active_orders_per_market=cfg.O,
+                 max_active_fills_per_market=cfg.F, num_customers=cfg.C)
+    market = aom.VecMarket(**shape, allow_extended_shapes=cfg.extended)
+    fills = market.new_fill_batch()
+    bbos = market.new_bbo_batch()
+
+    def step(mk, t):
+        mk.add_two_sided_quotes(*rows[t], fills)
+        if bbo:
+            mk.get_bbos(bbos)
+
+    for t in range(W):
+        step(market, t)
+    torch.cuda.synchronize()
+    snaps = [market.clone() for _ in range(3)]  # state at the start of the timed steps
+    torch.cuda.synchronize()
+    log(f"warm-up done ({W} steps); timing {K} steps")
+
+    # ---- A: throughput (the headline) ----
+    torch.cuda.synchronize()
+    a0 = time.perf_counter()
+    for t in range(W, T):
+        step(market, t)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - a0
+    log(f"A: {K} steps in {wall * 1e3:.2f} ms")
+
+    # ---- B: per-step latency (stream synced every step) ----
+    nlat = min(K, args.latency_steps)
+    lat = []
+    for t in range(W, W + nlat):
+        torch.cuda.synchronize()
+        h0 = time.perf_counter()
+        step(snaps[0], t)
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - h0)
+    lat_ms = np.array(lat) * 1e3
+
+    # ---- C: device time per kernel (HIP events on the launch stream) ----
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    torch.cuda.synchronize()
+    for i, t in enumerate(range(W, T)):
+        e = evs[i]
+        e[0].record()
+        snaps[1].add_two_sided_quotes(*rows[t], fills)
+        e[1].record()
+        if bbo:
+            snaps[1].get_bbos(bbos)
+        e[2].record()
+    torch.cuda.synchronize()
+    qm_ms = np.array([e[0].elapsed_time(e[1]) for e in evs])
+    bbo_ms = np.array([e[1].elapsed_time(e[2]) for e in evs]) if bbo else np.zeros(K)
+
+    # ---- D: exact work counts for the algorithmic bytes ----
+    counters = torch.zeros(4, dtype=torch.int64, device=dev)
+    snaps[2]._set_stats(counters)
+    for t in range(W, T):
+        snaps[2].add_two_sided_quotes(*rows[t], fills)
+    torch.cuda.synchronize()
+    n_ins, n_fill, n_empty, n_ovf = (int(x) for x in counters.cpu().tolist())
+    snaps[2]._set_stats(None)
+    log(f"work over {K} steps: inserts {n_ins}, fill rows {n_fill}, emptied {n_empty}, overflow {n_ovf}")
+
+    # algorithmic bytes (per launch of the matching kernel): quotes in 20 B + fill_counts 4 B
+    # per market; 32 B per accepted insert; 109 B per fill row; 8 B per emptied level.
+    qm_bytes = (24.0 * M * K + 32.0 * n_ins + 109.0 * n_fill + 8.0 * n_empty) / K
+    bbo_bytes = 24.0 * M  # 16 B out + 2 head-size reads of 4 B
+    qm_avg_s = float(qm_ms.mean()) * 1e-3
+    achieved = qm_bytes / qm_avg_s / 1e9
+
+    value = M * K / wall
+    result = {
+        "metric": "quote-matches/sec and market-steps/sec at 100k markets; p50 step latency",
+        "value": value,
+        "unit": "quote-matches/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": wall / K * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"config{cfg.index}_{cfg.name}",
+            "num_markets": M, "max_price_levels": cfg.L, "max_active_orders_per_market": cfg.O,
+            "max_active_fills_per_market": cfg.F, "num_customers": cfg.C,
+            "get_bbos_every_step": bbo, "parallelism": "single GPU, one lane per market",
+        },
+        "market_steps_per_s": K / wall,
+        "p50_step_latency_ms": float(np.percentile(lat_ms, 50)),
+        "p99_step_latency_ms": float(np.percentile(lat_ms, 99)),
+        "max_step_latency_ms": float(lat_ms.max()),
+        "device_ms_per_step": {"quote_match": float(qm_ms.mean()), "get_bbos": float(bbo_ms.mean())},
+        "work_per_step": {"inserts": n_ins / K, "fill_rows": n_fill / K, "levels_emptied": n_empty / K,
+                          "overflow_markets": n_ovf / K},
+        "roofline": {
+            "kernel": "quote_match_kernel",
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": qm_bytes,
+            "get_bbos_algorithmic_bytes_per_launch": bbo_bytes,
+        },
+    }
+
+    # ---- CPU baseline: the oracle on a bounded subset of the same workload ----
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args, cfg, host, M, W, K, bbo)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(args, cfg, host, M, W, K, bbo):
+    import numpy as np
+    from oracle.oracle import OracleMarket
+
+    model, avail = cpu_info()
+    nthreads = max(1, min(avail, 16))
+
+    def run(mc, threads, steps_timed):
+        o = OracleMarket(mc, cfg.L, cfg.O, cfg.F, cfg.C)
+        f = o.new_fill_batch()
+        b = o.new_bbo_batch()
+        sl = [np.ascontiguousarray(a[:, :mc]) for a in host]
+        for t in range(W):
+            o.add_two_sided_quotes(*(a[t] for a in sl), f, nthreads=threads)
+        c0 = time.perf_counter()
+        for t in range(W, W + steps_timed):
+            o.add_two_sided_quotes(*(a[t] for a in sl), f, nthreads=threads)
+            if bbo:
+                o.get_bbos(b, nthreads=threads)
+        return mc * steps_timed / (time.perf_counter() - c0)
+
+    # calibrate on a small sample, then size each leg to a bounded CPU time
+    rate_all = run(min(M, 2000), nthreads, min(K, 50))
+    mc_all = int(min(M, max(1000, rate_all * args.cpu_seconds / K)))
+    log(f"CPU leg: {mc_all} markets x {K} timed steps on {nthreads} threads")
+    v_all = run(mc_all, nthreads, K)
+    rate_one = run(min(M, 500), 1, min(K, 50))
+    mc_one = int(min(M, max(200, rate_one * (args.cpu_seconds / 3) / K)))
+    log(f"CPU leg: {mc_one} markets x {K} timed steps on 1 thread")
+    v_one = run(mc_one, 1, K)
+    return {
+        "value": v_all,
+        "unit": "quote-matches/s",
+        "cores": nthreads,
+        "kind": "port",
+        "sample": (f"markets 0..{mc_all - 1} of the same config-{cfg.index} stream, the same "
+                   f"{W} warm-up + {K} timed steps" + (" with get_bbos every step" if bbo else "")),
+        "single_thread_value": v_one,
+        "single_thread_sample": f"markets 0..{mc_one - 1}, same steps",
+        "host_cpu": model,
+        "host_cpus_available": avail,
+    }
+
+
+if __name__ == "__main__":
+    main()

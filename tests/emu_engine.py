@@ -1,0 +1,199 @@
+"""The engine's own per-market code, compiled for the host, behind the same C ABI.
+
+``csrc/market.hip`` built with ``-DASTRA_HOST_EMULATION --cuda-host-only`` runs
+every kernel body (the same __host__ __device__ functions the GPU runs) as a
+plain loop over host memory. ``EmuMarket`` drives that build through the
+prototypes of ``astra_cuda._native`` with numpy buffers standing in for device
+memory, so the CPU test suite checks the engine's logic, data layout and
+bounds against the oracle without a GPU. Test infrastructure only.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+BUILD_DIR = os.path.join(HERE, "_build")
+EMU_LIB = os.path.join(BUILD_DIR, "libastra_market_emu.so")
+SRC = os.path.join(ROOT, "astra-cuda_amd", "csrc", "market.hip")
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    if not force and os.path.exists(EMU_LIB) and os.path.getmtime(EMU_LIB) >= os.path.getmtime(SRC):
+        return EMU_LIB
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    from astra_cuda.build import hipcc
+    cmd = [hipcc(), "-DASTRA_HOST_EMULATION", "--cuda-host-only", "-O2", "-g", "-std=c++17",
+           "-fPIC", "-shared", f"-I{os.path.join(ROOT, 'include')}", SRC, "-o", EMU_LIB + ".tmp"]
+    subprocess.run(cmd, check=True, capture_output=True)
+    os.replace(EMU_LIB + ".tmp", EMU_LIB)
+    return EMU_LIB
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        from astra_cuda._native import PROTOTYPES
+        L = ctypes.CDLL(build())
+        for name, (res, args) in PROTOTYPES.items():
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc:
+        raise RuntimeError("Astra Fatal Error: " + lib().astra_last_error().decode())
+
+
+def _aligned(nbytes: int) -> np.ndarray:
+    raw = np.zeros(nbytes + 256, dtype=np.uint8)
+    off = (-raw.ctypes.data) % 256
+    return raw[off:off + nbytes]
+
+
+class EmuFills:
+    FIELDS = ("fill_prices", "fill_sizes", "fill_customer_ids", "fill_quoter_ids",
+              "fill_is_sell_quote", "fill_quote_sizes", "fill_tid", "fill_quote_tid", "fill_counts")
+
+    def __init__(self, M, F):
+        for f in self.FIELDS:
+            if f == "fill_counts":
+                setattr(self, f, np.zeros((M,), np.int32))
+            elif f == "fill_is_sell_quote":
+                setattr(self, f, np.zeros((M, F), np.bool_))
+            else:
+                setattr(self, f, np.zeros((M, F), np.int32))
+
+    def ptrs(self):
+        return [getattr(self, f).ctypes.data for f in self.FIELDS]
+
+
+class EmuBBO:
+    FIELDS = ("best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes", "last_prices")
+
+    def __init__(self, M):
+        for f in self.FIELDS:
+            setattr(self, f, np.zeros((M,), np.int32))
+
+
+class EmuMarket:
+    def __init__(self, M, L, O, F, C, extended=None, _src=None):
+        self.M, self.L, self.O, self.F, self.C = M, L, O, F, C
+        if extended is None:
+            extended = L > 128 or O > 1024 or F > 1024 or C > 1024
+        self.flags = 1 if extended else 0
+        n = ctypes.c_size_t()
+        _check(lib().astra_market_workspace_size(M, L, O, F, C, self.flags, ctypes.byref(n)))
+        self.ws = _aligned(max(int(n.value), 256))
+        h = ctypes.c_void_p()
+        if _src is None:
+            _check(lib().astra_market_create(M, L, O, F, C, 0, 64, self.flags, self.ws.ctypes.data,
+                                             self.ws.nbytes, None, ctypes.byref(h)))
+        else:
+            _check(lib().astra_market_clone(_src.h, self.ws.ctypes.data, self.ws.nbytes, None,
+                                            ctypes.byref(h)))
+        self.h = h
+        p = ctypes.c_void_p()
+        _check(lib().astra_market_portfolios(self.h, ctypes.byref(p)))
+        off = p.value - self.ws.ctypes.data
+        self.portfolios = self.ws[off:off + M * C * 8].view(np.int32).reshape(M, C, 2)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().astra_market_destroy(self.h)
+            self.h = None
+
+    def clone(self):
+        return EmuMarket(self.M, self.L, self.O, self.F, self.C, bool(self.flags), _src=self)
+
+    def new_fill_batch(self):
+        return EmuFills(self.M, self.F)
+
+    def new_bbo_batch(self):
+        return EmuBBO(self.M)
+
+    def add_two_sided_quotes(self, bid_px, bid_sz, ask_px, ask_sz, cust, fills):
+        ins = [np.ascontiguousarray(a, np.int32) for a in (bid_px, bid_sz, ask_px, ask_sz, cust)]
+        _check(lib().astra_market_add_two_sided_quotes(self.h, *[a.ctypes.data for a in ins],
+                                                        *fills.ptrs(), None))
+
+    def get_bbos(self, b):
+        _check(lib().astra_market_get_bbos(self.h, b.best_bid_prices.ctypes.data,
+                                           b.best_bid_sizes.ctypes.data, b.best_ask_prices.ctypes.data,
+                                           b.best_ask_sizes.ctypes.data, None))
+
+    def update_last_prices(self, b, fills):
+        _check(lib().astra_update_last_prices(b.last_prices.ctypes.data, fills.fill_counts.ctypes.data,
+                                              fills.fill_prices.ctypes.data, self.M, self.F, None))
+
+    def reset(self):
+        _check(lib().astra_market_reset(self.h, None))
+
+    def clear_quotes(self, mask):
+        m = np.ascontiguousarray(mask, np.bool_)
+        _check(lib().astra_market_clear_quotes(self.h, m.ctypes.data, None))
+
+    def to_string(self, market_id):
+        need = ctypes.c_size_t()
+        buf = ctypes.create_string_buffer(1 << 16)
+        _check(lib().astra_market_to_string(self.h, int(market_id), buf, 1 << 16, ctypes.byref(need), None))
+        if need.value >= (1 << 16):
+            buf = ctypes.create_string_buffer(need.value + 1)
+            _check(lib().astra_market_to_string(self.h, int(market_id), buf, need.value + 1,
+                                                ctypes.byref(need), None))
+        return buf.value.decode()
+
+    def set_stats(self, counters):
+        _check(lib().astra_market_set_stats(self.h, None if counters is None else counters.ctypes.data))
+
+    @property
+    def global_tid(self):
+        v = ctypes.c_int32()
+        _check(lib().astra_market_get_tid(self.h, ctypes.byref(v)))
+        return v.value
+
+
+class EmuAdapter:
+    """KAT adapter (tests/kat_harness.py) over the emulation build."""
+
+    def __init__(self, shape):
+        self.mk = EmuMarket(shape["M"], shape["L"], shape["O"], shape["F"], shape["C"])
+        self.fills = self.mk.new_fill_batch()
+        self.bbo = self.mk.new_bbo_batch()
+
+    def quote(self, *args):
+        self.mk.add_two_sided_quotes(*args, self.fills)
+
+    def bbos(self):
+        self.mk.get_bbos(self.bbo)
+
+    def update_last(self):
+        self.mk.update_last_prices(self.bbo, self.fills)
+
+    def reset(self):
+        self.mk.reset()
+
+    def bbo_reset(self):
+        for f in EmuBBO.FIELDS:
+            getattr(self.bbo, f)[:] = 0
+
+    def new_bbo(self):
+        self.bbo = self.mk.new_bbo_batch()
+
+    def array(self, name):
+        if name == "portfolio":
+            return self.mk.portfolios.copy()
+        if name in EmuBBO.FIELDS:
+            return getattr(self.bbo, name).copy()
+        return getattr(self.fills, name).copy()
+
+    def to_string(self, m):
+        return self.mk.to_string(m)

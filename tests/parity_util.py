@@ -1,0 +1,143 @@
+"""Shared helpers for the GPU parity tests: the HIP engine (through the drop-in
+``astra_cuda.order_matching`` API) against the CPU oracle on the same inputs."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from kat_harness import BBO_FIELDS, FILL_FIELDS
+
+DEV = "cuda:0"
+
+
+def t32(a) -> torch.Tensor:
+    return torch.as_tensor(np.ascontiguousarray(a, dtype=np.int32)).to(DEV)
+
+
+class GpuAdapter:
+    """KAT adapter over astra_cuda.order_matching (the product path)."""
+
+    def __init__(self, shape):
+        from astra_cuda import order_matching as aom
+        ext = shape["L"] > 128 or shape["O"] > 1024 or shape["F"] > 1024 or shape["C"] > 1024
+        self.mk = aom.VecMarket(shape["M"], shape["L"], shape["O"], shape["F"], shape["C"],
+                                allow_extended_shapes=ext)
+        self.fills = self.mk.new_fill_batch()
+        self.bbo = self.mk.new_bbo_batch()
+
+    def quote(self, bid_px, bid_sz, ask_px, ask_sz, cust):
+        self.mk.add_two_sided_quotes(t32(bid_px), t32(bid_sz), t32(ask_px), t32(ask_sz), t32(cust),
+                                     self.fills)
+
+    def bbos(self):
+        self.mk.get_bbos(self.bbo)
+
+    def update_last(self):
+        self.bbo.update_last_prices(self.fills)
+
+    def reset(self):
+        self.mk.reset()
+
+    def bbo_reset(self):
+        self.bbo.reset()
+
+    def new_bbo(self):
+        self.bbo = self.mk.new_bbo_batch()
+
+    def array(self, name):
+        if name == "portfolio":
+            return self.mk.get_customer_portfolios().cpu().numpy()
+        if name in BBO_FIELDS:
+            return getattr(self.bbo, name).cpu().numpy()
+        return getattr(self.fills, name).cpu().numpy()
+
+    def to_string(self, m):
+        return self.mk.to_string(m)
+
+
+def effective_counts(counts: np.ndarray, F: int) -> np.ndarray:
+    """Number of fill rows written by the last call (F for an overflowed market)."""
+    return np.where(counts < 0, F, counts)
+
+
+def compare_fills(gpu_fills, ora_fills, F: int, where: str, full: bool = False) -> int:
+    """Compare the rows written by the last call (or the full arrays when ``full``).
+    Returns the number of fill rows compared."""
+    gc = gpu_fills.fill_counts.cpu().numpy()
+    oc = ora_fills.fill_counts
+    if not np.array_equal(gc, oc):
+        bad = np.nonzero(gc != oc)[0][:5]
+        raise AssertionError(f"{where}: fill_counts differ at markets {bad.tolist()}: "
+                             f"gpu {gc[bad].tolist()} oracle {oc[bad].tolist()}")
+    eff = effective_counts(oc, F)
+    kmax = F if full else int(eff.max(initial=0))
+    if kmax == 0:
+        return 0
+    valid = np.arange(kmax)[None, :] < eff[:, None]
+    for f in FILL_FIELDS:
+        g = getattr(gpu_fills, f)[:, :kmax].cpu().numpy()
+        o = getattr(ora_fills, f)[:, :kmax]
+        if full:
+            ok = np.array_equal(g, o)
+        else:
+            ok = np.array_equal(np.where(valid, g, 0), np.where(valid, o, 0))
+        if not ok:
+            diff = np.argwhere((g != o) & (True if full else valid))[:5]
+            raise AssertionError(f"{where}: {f} differs at {diff.tolist()}: "
+                                 f"gpu {[g[tuple(d)] for d in diff]} oracle {[o[tuple(d)] for d in diff]}")
+    return int(eff.sum())
+
+
+def compare_bbo(gpu_bbo, ora_bbo, where: str):
+    for f in ("best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes", "last_prices"):
+        g = getattr(gpu_bbo, f).cpu().numpy()
+        o = getattr(ora_bbo, f)
+        if not np.array_equal(g, o):
+            bad = np.nonzero(g != o)[0][:5]
+            raise AssertionError(f"{where}: {f} differs at {bad.tolist()}: gpu {g[bad].tolist()} "
+                                 f"oracle {o[bad].tolist()}")
+
+
+def compare_portfolios(gpu_mk, ora_mk, where: str):
+    g = gpu_mk.get_customer_portfolios().cpu().numpy()
+    o = ora_mk.customer_portfolios
+    if not np.array_equal(g, o):
+        bad = np.argwhere(g != o)[:5]
+        raise AssertionError(f"{where}: portfolios differ at {bad.tolist()}")
+
+
+def run_parity(M, L, O, F, C, steps, gen, *, bbo_every=1, full_every=0, last_every=1,
+               extended=None, nthreads=8, label=""):
+    """Drive GPU engine and oracle with the same inputs; compare after every step.
+
+    ``gen(t)`` returns (bid_px, bid_sz, ask_px, ask_sz, cust) int32 arrays of shape [M].
+    Returns summary statistics (fill rows compared, overflows seen).
+    """
+    from astra_cuda import order_matching as aom
+    from oracle.oracle import OracleMarket
+    if extended is None:
+        extended = L > 128 or O > 1024 or F > 1024 or C > 1024
+    g = aom.VecMarket(M, L, O, F, C, allow_extended_shapes=extended)
+    gf, gb = g.new_fill_batch(), g.new_bbo_batch()
+    o = OracleMarket(M, L, O, F, C)
+    of, ob = o.new_fill_batch(), o.new_bbo_batch()
+    rows = overflows = 0
+    for t in range(steps):
+        args = gen(t)
+        where = f"{label} step {t}"
+        g.add_two_sided_quotes(*(t32(a) for a in args), gf)
+        o.add_two_sided_quotes(*args, of, nthreads=nthreads)
+        full = bool(full_every) and (t % full_every == full_every - 1 or t == steps - 1)
+        rows += compare_fills(gf, of, F, where, full=full)
+        overflows += int((of.fill_counts < 0).sum())
+        if last_every and t % last_every == 0:
+            gb.update_last_prices(gf)
+            o.update_last_prices(ob, of)
+        if bbo_every and t % bbo_every == 0:
+            g.get_bbos(gb)
+            o.get_bbos(ob, nthreads=nthreads)
+            compare_bbo(gb, ob, where)
+        if t % 50 == 0 or t == steps - 1:
+            compare_portfolios(g, o, where)
+    assert g.global_tid == o.global_tid
+    return {"fill_rows": rows, "overflows": overflows, "gpu": g, "oracle": o}

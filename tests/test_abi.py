@@ -1,0 +1,91 @@
+"""The C-ABI library loads, exports what include/astra_market.h declares, and
+validates shapes like the reference constructor (CPU only: no device calls)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "astra_market.h")
+
+
+def _ensure_built():
+    from astra_cuda.build import LIB_PATH, build
+    if not os.path.exists(LIB_PATH):
+        build()
+    return LIB_PATH
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(astra_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for must in ("astra_market_create", "astra_market_add_two_sided_quotes", "astra_market_get_bbos",
+                 "astra_update_last_prices", "astra_market_reset", "astra_market_clear_quotes",
+                 "astra_market_clone", "astra_market_to_string", "astra_market_portfolios"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_ensure_built())
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_prototypes_cover_header():
+    from astra_cuda._native import PROTOTYPES
+    assert sorted(PROTOTYPES) == _declared()
+
+
+def _ws(*shape, flags=0):
+    from astra_cuda import _native
+    n = ctypes.c_size_t(0)
+    rc = _native.lib().astra_market_workspace_size(*shape, flags, ctypes.byref(n))
+    return rc, n.value, _native.last_error()
+
+
+def test_workspace_size_and_reference_caps():
+    rc, n, _ = _ws(10, 128, 1024, 512, 16)
+    assert rc == 0 and n > 0
+    # market.cu:338-342: L <= 128, O <= 1024, F <= 1024, C <= 1024
+    for shape, text in (((10, 129, 1024, 512, 16), "max_price_levels <= ASTRA_PRICE_LEVELS"),
+                        ((10, 128, 1025, 512, 16), "<= ASTRA_MAX_ACTIVE_ORDERS_PER_MARKET"),
+                        ((10, 128, 1024, 1025, 16), "<= ASTRA_MAX_ACTIVE_FILLS_PER_MARKET"),
+                        ((10, 128, 1024, 512, 1025), "<= ASTRA_MAX_CUSTOMERS"),
+                        ((2048 * 2048 + 1, 128, 16, 16, 16), "<= ASTRA_MAX_MARKETS")):
+        rc, _, msg = _ws(*shape)
+        assert rc == 1, shape
+        assert text.split()[-1] in msg and "=" in msg, msg
+
+
+def test_extended_shapes_flag():
+    rc, _, _ = _ws(20000, 512, 4096, 4096, 64)
+    assert rc == 1
+    rc, n, _ = _ws(20000, 512, 4096, 4096, 64, flags=1)
+    assert rc == 0
+    # records dominate: 16 bytes per order slot
+    assert n >= 20000 * 4096 * 16
+
+
+def test_constants_match_reference():
+    from astra_cuda import order_matching as aom  # market.h:56-61, test_vec_market.py:36-39
+    assert aom.MAX_MARKETS == 2048 * 2048
+    assert aom.PRICE_LEVELS == 128
+    assert aom.MAX_ACTIVE_ORDERS_PER_MARKET == 1024
+    assert aom.MAX_ACTIVE_FILLS_PER_MARKET == 1024
+    assert aom.NULL_INDEX == -1
+    assert aom.MAX_CUSTOMERS == 1024
+
+
+def test_no_device_fails_loudly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    from astra_cuda import order_matching as aom
+    with pytest.raises(RuntimeError, match="Astra Fatal Error"):
+        aom.VecMarket(4, 128, 16, 16)

@@ -1,0 +1,226 @@
+"""HIP engine vs the CPU oracle, bit-exact (GPU).
+
+Everything goes through the drop-in API (astra_cuda.order_matching, i.e. the
+C ABI in libastra_market.so). Bar: every fill field of every row a call wrote,
+fill_counts, BBOs, last prices and portfolios are identical to the oracle's on
+the same inputs, after every step.
+"""
+import numpy as np
+import pytest
+import torch
+
+from kat_harness import load_kats, run_scenario
+from parity_util import DEV, GpuAdapter, compare_bbo, compare_fills, compare_portfolios, run_parity, t32
+
+pytestmark = pytest.mark.gpu
+
+SCENARIOS = load_kats()
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("sc", SCENARIOS, ids=[s["name"] for s in SCENARIOS])
+def test_gpu_kat(sc):
+    _log(f"kat {sc['name']}")
+    run_scenario(sc, GpuAdapter)
+
+
+def test_gpu_library_is_the_in_tree_build():
+    import astra_cuda._native as nat
+    lib = nat.lib()
+    assert lib._name.endswith("astra_cuda/libastra_market.so")
+
+
+def _stream_gen(cfg_index, markets=None, M_override=None):
+    from astra_cuda.workloads import CONFIGS, QuoteStream
+    cfg = CONFIGS[cfg_index]
+    qs = QuoteStream(cfg, markets)
+    return cfg, qs.step
+
+
+def test_gpu_config1_full_run():
+    """Config 1 exactly as specified (64 markets x 1000 steps, ring wraps at step 512)."""
+    cfg, gen = _stream_gen(1)
+    _log("config 1: 64 x 1000")
+    r = run_parity(cfg.M, cfg.L, cfg.O, cfg.F, cfg.C, cfg.steps, gen, full_every=100, label="cfg1")
+    # config 1 quotes never self-cross, but resting orders do cross later quotes
+    assert r["fill_rows"] > 0
+
+
+def test_gpu_config2_subset():
+    cfg, gen = _stream_gen(2, np.arange(3000))
+    _log("config 2 subset: 3000 x 400")
+    r = run_parity(3000, cfg.L, cfg.O, cfg.F, cfg.C, 400, gen, full_every=200, label="cfg2")
+    assert r["fill_rows"] > 3000
+
+
+def test_gpu_config3_subset_with_eviction():
+    """Config 3 markets 0..3999 for all 1000 steps (the ring of 1024 wraps after 512 steps)."""
+    cfg, gen = _stream_gen(3, np.arange(4000))
+    _log("config 3 subset: 4000 x 1000")
+    r = run_parity(4000, cfg.L, cfg.O, cfg.F, cfg.C, 1000, gen, bbo_every=1, full_every=250,
+                   label="cfg3")
+    assert r["fill_rows"] > 4000
+
+
+def test_gpu_config4_subset_deep_book():
+    """Config 4 shape (L=512: 8 mask words, O=F=4096, C=64) on 300 markets x 2000 steps."""
+    cfg, gen = _stream_gen(4, np.arange(300))
+    _log("config 4 subset: 300 x 2000")
+    r = run_parity(300, cfg.L, cfg.O, cfg.F, cfg.C, 2000, gen, bbo_every=5, full_every=500,
+                   label="cfg4")
+    assert r["fill_rows"] > 300
+
+
+# (M, L, O, F, C, steps, seed): tiny rings and fill caps force eviction aliasing,
+# self links, zero/negative fills and overflow; prices/sizes/customers include
+# rejected and out-of-range values. L covers 1, 2, 4, 8 and 16 mask words.
+ALIAS_CASES = [
+    (257, 8, 1, 3, 3, 200, 11),
+    (257, 8, 2, 4, 3, 200, 12),
+    (300, 16, 3, 2, 4, 200, 13),
+    (300, 70, 5, 6, 4, 300, 14),
+    (300, 128, 7, 16, 5, 300, 15),
+    (200, 200, 9, 5, 3, 300, 16),
+    (200, 512, 6, 8, 70, 300, 17),
+    (150, 1000, 11, 9, 3, 300, 18),
+]
+
+
+@pytest.mark.parametrize("M,L,O,F,C,steps,seed", ALIAS_CASES)
+def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed):
+    _log(f"aliasing M={M} L={L} O={O} F={F}")
+    rng = np.random.default_rng(seed)
+    hot = max(4, min(L, 24))  # concentrate prices so books cross often
+
+    def gen(t):
+        base = rng.integers(0, max(1, L - hot), 1)[0]
+        bid = (base + rng.integers(-1, hot + 1, M)).astype(np.int32)
+        ask = (base + rng.integers(-1, hot + 1, M)).astype(np.int32)
+        bid[rng.random(M) < 0.02] = L  # rejected: price >= L
+        ask[rng.random(M) < 0.02] = -1  # rejected here: negative price
+        return (bid, rng.integers(-1, 8, M).astype(np.int32), ask,
+                rng.integers(-1, 8, M).astype(np.int32), rng.integers(-1, C + 2, M).astype(np.int32))
+
+    r = run_parity(M, L, O, F, C, steps, gen, full_every=50, label=f"alias L{L} O{O}")
+    if O <= 3:
+        assert r["overflows"] > 0
+
+
+def test_gpu_reset_clear_clone_and_to_string():
+    """Reset / ClearQuotes / copy constructor / ToString interleaved with trading."""
+    from astra_cuda import order_matching as aom
+    from oracle.oracle import OracleMarket
+    M, L, O, F, C = 97, 40, 6, 12, 5
+    rng = np.random.default_rng(7)
+    g = aom.VecMarket(M, L, O, F, C)
+    o = OracleMarket(M, L, O, F, C)
+    gf, of = g.new_fill_batch(), o.new_fill_batch()
+    gb, ob = g.new_bbo_batch(), o.new_bbo_batch()
+
+    def step(gm, om, t):
+        args = (rng.integers(0, L, M).astype(np.int32), rng.integers(0, 6, M).astype(np.int32),
+                rng.integers(0, L, M).astype(np.int32), rng.integers(0, 6, M).astype(np.int32),
+                rng.integers(0, C, M).astype(np.int32))
+        gm.add_two_sided_quotes(*(t32(a) for a in args), gf)
+        om.add_two_sided_quotes(*args, of)
+        compare_fills(gf, of, F, f"step {t}")
+
+    for t in range(300):
+        step(g, o, t)
+        if t % 37 == 5:
+            mask = rng.random(M) < 0.3
+            g.clear_quotes(torch.as_tensor(mask).to(DEV))
+            o.clear_quotes(mask)
+        if t == 150:
+            g.reset()
+            o.reset()
+        if t % 25 == 0:
+            g.get_bbos(gb)
+            o.get_bbos(ob)
+            compare_bbo(gb, ob, f"step {t}")
+            compare_portfolios(g, o, f"step {t}")
+            for m in (0, 1, M // 2, M - 1):
+                assert g.to_string(m) == o.to_string(m), (t, m)
+    assert g.to_string(M) == o.to_string(M)
+    # copy constructor: the clone continues identically and independently
+    g2, o2 = g.clone(), o.clone()
+    assert g2.global_tid == o2.global_tid == g.global_tid
+    for t in range(300, 340):
+        step(g2, o2, t)
+    compare_portfolios(g2, o2, "clone")
+    g2.get_bbos(gb)
+    o2.get_bbos(ob)
+    compare_bbo(gb, ob, "clone")
+    # the original is untouched by the clone's trading
+    g.get_bbos(gb)
+    o.get_bbos(ob)
+    compare_bbo(gb, ob, "original after clone")
+    compare_portfolios(g, o, "original after clone")
+
+
+def test_gpu_portfolio_view_is_live_and_copy_to():
+    from astra_cuda import order_matching as aom
+    g = aom.VecMarket(3, 128, 64, 16)
+    f = g.new_fill_batch()
+    view = g.get_customer_portfolios()
+    one = torch.ones(3, dtype=torch.int32, device=DEV)
+    g.add_two_sided_quotes(one * 50, one * 10, one * 0, one * 0, one * 0, f)
+    g.add_two_sided_quotes(one * 0, one * 0, one * 50, one * 4, one * 1, f)
+    assert view.data_ptr() == g.get_customer_portfolios().data_ptr()
+    assert view[:, 0].tolist() == [[4, -200]] * 3 and view[:, 1].tolist() == [[-4, 200]] * 3
+    buf = torch.zeros(3, 16, 2, dtype=torch.int32, device=DEV)
+    g.copy_customer_portfolios_to(buf)
+    assert torch.equal(buf, view)
+    with pytest.raises(RuntimeError, match="Astra Fatal Error"):
+        g.copy_customer_portfolios_to(torch.zeros(3, 15, 2, dtype=torch.int32, device=DEV))
+
+
+def test_gpu_current_stream_is_used():
+    """Work issued inside a torch stream context runs on that stream, in order."""
+    from astra_cuda import order_matching as aom
+    from oracle.oracle import OracleMarket
+    M, L, O, F, C = 2000, 128, 64, 32, 16
+    rng = np.random.default_rng(3)
+    g = aom.VecMarket(M, L, O, F, C)
+    o = OracleMarket(M, L, O, F, C)
+    gf, of = g.new_fill_batch(), o.new_fill_batch()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for t in range(50):
+            args = [rng.integers(0, L, M), rng.integers(1, 9, M), rng.integers(0, L, M),
+                    rng.integers(1, 9, M), rng.integers(0, C, M)]
+            args = [a.astype(np.int32) for a in args]
+            ins = [torch.as_tensor(a).to(DEV, non_blocking=False) for a in args]
+            g.add_two_sided_quotes(*ins, gf)
+            o.add_two_sided_quotes(*args, of)
+        s.synchronize()
+    compare_fills(gf, of, F, "stream")
+    compare_portfolios(g, o, "stream")
+
+
+def test_gpu_input_validation_errors():
+    from astra_cuda import order_matching as aom
+    g = aom.VecMarket(4, 128, 64, 16)
+    f = g.new_fill_batch()
+    ok = torch.zeros(4, dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match=r"bid_px.size\(0\) == num_markets_"):
+        g.add_two_sided_quotes(torch.zeros(5, dtype=torch.int32, device=DEV), ok, ok, ok, ok, f)
+    with pytest.raises(RuntimeError, match="ask_px tensor must be on device 0"):
+        g.add_two_sided_quotes(ok, ok, torch.zeros(4, dtype=torch.int32), ok, ok, f)
+    with pytest.raises(RuntimeError, match="customer_ids tensor must be contiguous"):
+        g.add_two_sided_quotes(ok, ok, ok, ok, torch.zeros(8, dtype=torch.int32, device=DEV)[::2], f)
+    with pytest.raises(RuntimeError, match="must be int32"):
+        g.add_two_sided_quotes(ok, ok.long(), ok, ok, ok, f)
+    with pytest.raises(RuntimeError, match="Astra Fatal Error"):
+        aom.VecMarket(4, 129, 64, 16)  # market.cu:339
+    with pytest.raises(RuntimeError, match="Astra Fatal Error"):
+        aom.VecMarket(4, 128, 64, 16, threads_per_block=0)  # market.cu:343
+    with pytest.raises(RuntimeError, match="Astra Fatal Error"):
+        aom.VecMarket(4, 128, 64, 16, device_id=torch.cuda.device_count())  # market.cu:350
+    with pytest.raises(RuntimeError, match="reset_indices"):
+        g.clear_quotes(torch.zeros(4, dtype=torch.int32, device=DEV))
+    # no state change from the rejected calls: TID still 0
+    assert g.global_tid == 0
