@@ -425,13 +425,15 @@ class VecMarket:
     # -- introspection (not in the reference binding) -------------------------
 
     def _set_stats(self, counters) -> None:
-        """Diagnostic: accumulate per-call work counts into an int64 [4] device tensor
-        (inserts, fill rows, emptied levels, overflowed markets); None switches it off."""
+        """Diagnostic: accumulate per-call work counts into an int64 [8] device tensor
+        (inserts, fill rows, emptied levels, overflowed markets, fast-forwarded
+        overflows); None switches it off."""
         if counters is None:
             _check(self._lib.astra_market_set_stats(self._h, None))
             return
-        if counters.dtype != torch.int64 or counters.numel() < 4 or counters.device != self._device:
-            _fatal("stats counters must be an int64 tensor of >= 4 elements on the engine's device")
+        if (counters.dtype != torch.int64 or counters.numel() < 8 or counters.device != self._device
+                or not counters.is_contiguous()):
+            _fatal("stats counters must be a contiguous int64 tensor of >= 8 elements on the engine's device")
         self._stats_ref = counters
         _check(self._lib.astra_market_set_stats(self._h, counters.data_ptr()))
 

@@ -141,7 +141,7 @@ inline int mask_words_for(int32_t L) {
 // Byte offsets of the book arrays inside the workspace.
 struct Layout {
   int W;
-  size_t masks, next_slot, levels, records, portfolios, total;
+  size_t masks, next_slot, bbo, levels, records, portfolios, total;
 };
 
 Layout make_layout(int64_t M, int64_t L, int64_t O, int64_t C) {
@@ -152,6 +152,8 @@ Layout make_layout(int64_t M, int64_t L, int64_t O, int64_t C) {
   off = align_up(off + (size_t)2 * l.W * M * 8, 256);
   l.next_slot = off;
   off = align_up(off + (size_t)M * 4, 256);
+  l.bbo = off;
+  off = align_up(off + (size_t)4 * M * 4, 256);
   l.levels = off;
   off = align_up(off + (size_t)M * L * 8, 256);
   l.records = off;
@@ -182,6 +184,7 @@ namespace {
 struct Book {
   uint64_t *masks;            // [2][W][M]: side 0 = bid, 1 = ask
   int32_t *next_slot;         // [M], in [0, O)
+  int32_t *bbo;               // [4][M]: best bid price, size, best ask price, size
   uint16_t *levels;           // [M][L][4] = {bid_head, bid_tail, ask_head, ask_tail}
   uint4 *records;             // [M][O] = {size, customer, tid, price | next << 16}
   int32_t *portfolios;        // [M][C][2] = {contracts, cash}
@@ -193,6 +196,7 @@ Book book_of(const astra_market *h) {
   Book b;
   b.masks = reinterpret_cast<uint64_t *>(h->ws + h->lay.masks);
   b.next_slot = reinterpret_cast<int32_t *>(h->ws + h->lay.next_slot);
+  b.bbo = reinterpret_cast<int32_t *>(h->ws + h->lay.bbo);
   b.levels = reinterpret_cast<uint16_t *>(h->ws + h->lay.levels);
   b.records = reinterpret_cast<uint4 *>(h->ws + h->lay.records);
   b.portfolios = reinterpret_cast<int32_t *>(h->ws + h->lay.portfolios);
@@ -287,33 +291,78 @@ ASTRA_HD void mask_clear(uint64_t (&m)[W], int p) {
   for (int i = 0; i < W; ++i) m[i] &= ~((uint64_t)((p >> 6) == i) << (p & 63));
 }
 
-// Appends one order to the tail of its level list (market.cu:44-70 for the bid,
-// :73-99 for the ask). `word` is the side's {head, tail} pair read before any
-// store of this call; `side` is 0 (bid) or 1 (ask).
-template <int W>
-ASTRA_HD void insert_order(uint16_t *lv, uint4 *rec, uint64_t (&mask)[W], int32_t &ns, int32_t O,
-                           int side, int32_t price, int32_t size, int32_t cust, int32_t tid,
-                           uint32_t word) {
-  const int32_t slot = ns;
-  ns = (ns + 1 == O) ? 0 : ns + 1;
-  rec[slot] = make_uint4((uint32_t)size, (uint32_t)cust, (uint32_t)tid,
-                         (uint32_t)price | (kNull16 << 16));
-  const uint32_t old_tail = word >> 16;
-  uint16_t *pair = lv + (size_t)price * 4 + 2 * side;
-  if (old_tail == kNull16) {
-    *reinterpret_cast<uint32_t *>(pair) = (uint32_t)slot | ((uint32_t)slot << 16);
-    mask_set<W>(mask, price);
-  } else {
-    pair[1] = (uint16_t)slot;
-    if (old_tail < (uint32_t)O) reinterpret_cast<uint16_t *>(rec + old_tail)[7] = (uint16_t)slot;
+// Byte offsets of one side's {head, tail} pair within a level: side 0 = bid, 1 = ask.
+ASTRA_HD uint32_t level_word(const uint16_t *lv, int32_t price, int side) {
+  return *reinterpret_cast<const uint32_t *>(lv + (size_t)price * 4 + 2 * side);
+}
+
+ASTRA_HD void store_level_word(uint16_t *lv, int32_t price, int side, uint32_t w) {
+  *reinterpret_cast<uint32_t *>(lv + (size_t)price * 4 + 2 * side) = w;
+}
+
+ASTRA_HD void store_head(uint16_t *lv, int32_t price, int side, uint32_t head) {
+  lv[(size_t)price * 4 + 2 * side] = (uint16_t)head;
+}
+
+ASTRA_HD uint32_t rec_next(const uint4 &r) { return r.w >> 16; }
+ASTRA_HD uint4 with_next(uint4 r, uint32_t next) {
+  r.w = (r.w & kNull16) | (next << 16);
+  return r;
+}
+
+// Rows that a market still owes when its matching loop has reached a state that
+// repeats forever; the caller writes them (cooperatively on the GPU).
+struct Bulk {
+  int64_t base;   // first fill index (m * F + k)
+  int32_t count;  // rows to write
+  int32_t alt;    // 1: negate size and quote size on every odd row
+  int32_t v[8];   // price, size, taker, quoter, is_sell_quote, quote_size, tid, quote_tid
+};
+
+ASTRA_HD void write_fill(const FillOut &out, int64_t fi, const int32_t (&v)[8]) {
+  out.prices[fi] = v[0];
+  out.sizes[fi] = v[1];
+  out.taker[fi] = v[2];
+  out.quoter[fi] = v[3];
+  out.is_sell_quote[fi] = (uint8_t)v[4];
+  out.quote_sizes[fi] = v[5];
+  out.tid[fi] = v[6];
+  out.quote_tid[fi] = v[7];
+}
+
+// Host build: write the owed rows directly.
+inline void write_bulk_host(const FillOut &out, const Bulk &bk) {
+  for (int32_t k = 0; k < bk.count; ++k) {
+    int32_t v[8];
+    for (int i = 0; i < 8; ++i) v[i] = bk.v[i];
+    if (bk.alt && (k & 1)) {
+      v[1] = (int32_t)(0u - (uint32_t)v[1]);
+      v[5] = (int32_t)(0u - (uint32_t)v[5]);
+    }
+    write_fill(out, bk.base + k, v);
   }
 }
 
 // add_orders_kernel + match_orders_kernel (market.cu:17-100, 102-278) for
-// market m. STATS builds the diagnostic variant that also counts inserts, fill
-// rows, emptied levels and overflowed markets.
+// market m, followed by the best bid/offer of the resulting book (what
+// get_bbo_kernel, market.cu:280-320, would read), which is left in the
+// workspace's BBO cache. STATS builds the diagnostic variant that also counts
+// inserts, fill rows, emptied levels, overflowed markets and fast-forwards.
+//
+// Memory round trips are what a lane waits on, so: the two insert levels and
+// the two current best levels are read in one round trip, heads at loop entry
+// come from those words, the records just inserted come from registers, and the
+// next level of each side is read ahead while the current one is consumed.
+//
+// Two loop states repeat forever (both arise from ring-slot reuse): a size-0
+// head that links to itself (each pass emits the same zero-size fill and
+// changes nothing) and one slot heading both sides with size s != 0 (fills of
+// s and -s alternate). The reference loops until F fills and then writes -1;
+// here the owed rows are handed to the caller in `bulk`, the final state is set
+// directly, and the count is -1, which is the same result.
 template <int W, bool STATS>
-ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut &out, int64_t m) {
+ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut &out, int64_t m,
+                                 Bulk &bulk) {
   const int64_t M = b.M;
   const int32_t L = b.L, O = b.O, F = b.F, C = b.C;
 
@@ -331,49 +380,112 @@ ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut
   uint4 *rec = b.records + m * (int64_t)O;
   int32_t *pf = b.portfolios + m * (int64_t)C * 2;
 
-  // ---- add: bid first, then ask (TIDs base, base + 1) ----
   const bool bid_ok = bid_sz > 0 && (uint32_t)bid_px < (uint32_t)L;
   const bool ask_ok = ask_sz > 0 && (uint32_t)ask_px < (uint32_t)L;
-  // Both {head, tail} words are read up front: the bid insert only writes bid
-  // halves of level words, so the ask word it would have read is unchanged.
-  const uint32_t bword = bid_ok ? *reinterpret_cast<const uint32_t *>(lv + (size_t)bid_px * 4) : 0u;
-  const uint32_t aword =
-      ask_ok ? *reinterpret_cast<const uint32_t *>(lv + (size_t)ask_px * 4 + 2) : 0u;
-  if (bid_ok) insert_order<W>(lv, rec, bm, ns, O, 0, bid_px, bid_sz, cust, in.base_tid, bword);
-  if (ask_ok)
-    insert_order<W>(lv, rec, am, ns, O, 1, ask_px, ask_sz, cust,
-                    (int32_t)((uint32_t)in.base_tid + 1u), aword);
+  const int bb0 = mask_highest<W>(bm);
+  const int ba0 = mask_lowest<W>(am, L);
+  // One round trip for the four level words this call may start from. The bid
+  // insert only writes bid halves of level words, so the ask words read here
+  // are the ones the ask insert would have read after it.
+  const uint32_t bword = bid_ok ? level_word(lv, bid_px, 0) : 0u;
+  const uint32_t aword = ask_ok ? level_word(lv, ask_px, 1) : 0u;
+  const uint32_t bbw0 = bb0 >= 0 ? level_word(lv, bb0, 0) : 0xFFFFFFFFu;
+  const uint32_t baw0 = ba0 < L ? level_word(lv, ba0, 1) : 0xFFFFFFFFu;
 
-  // ---- match while the book is crossed (market.cu:145-274) ----
+  // ---- add: bid first, then ask (market.cu:44-70, 73-99) ----
+  // krb / kra track the two inserted records as stored, including later writes
+  // of their next fields, so the first match pass can use them unread.
+  uint32_t bslot = 0xFFFFFFFFu, aslot = 0xFFFFFFFFu;
+  uint4 krb = make_uint4(0, 0, 0, 0), kra = make_uint4(0, 0, 0, 0);
+  if (bid_ok) {
+    bslot = (uint32_t)ns;
+    ns = (ns + 1 == O) ? 0 : ns + 1;
+    krb = make_uint4((uint32_t)bid_sz, (uint32_t)cust, (uint32_t)in.base_tid,
+                     (uint32_t)bid_px | (kNull16 << 16));
+    rec[bslot] = krb;
+    const uint32_t old_tail = bword >> 16;
+    if (old_tail == kNull16) {
+      store_level_word(lv, bid_px, 0, bslot | (bslot << 16));
+      mask_set<W>(bm, bid_px);
+    } else {
+      lv[(size_t)bid_px * 4 + 1] = (uint16_t)bslot;
+      if (old_tail < (uint32_t)O) {
+        reinterpret_cast<uint16_t *>(rec + old_tail)[7] = (uint16_t)bslot;
+        if (old_tail == bslot) krb = with_next(krb, bslot);
+      }
+    }
+  }
+  if (ask_ok) {
+    aslot = (uint32_t)ns;
+    ns = (ns + 1 == O) ? 0 : ns + 1;
+    kra = make_uint4((uint32_t)ask_sz, (uint32_t)cust, (uint32_t)((uint32_t)in.base_tid + 1u),
+                     (uint32_t)ask_px | (kNull16 << 16));
+    rec[aslot] = kra;
+    if (aslot == bslot) krb = kra;  // O == 1: the ask reused the bid's slot
+    const uint32_t old_tail = aword >> 16;
+    if (old_tail == kNull16) {
+      store_level_word(lv, ask_px, 1, aslot | (aslot << 16));
+      mask_set<W>(am, ask_px);
+    } else {
+      lv[(size_t)ask_px * 4 + 3] = (uint16_t)aslot;
+      if (old_tail < (uint32_t)O) {
+        reinterpret_cast<uint16_t *>(rec + old_tail)[7] = (uint16_t)aslot;
+        if (old_tail == bslot) krb = with_next(krb, aslot);
+        if (old_tail == aslot) kra = with_next(kra, aslot);
+      }
+    }
+  }
+
+  // ---- heads of the best levels, known without another read ----
   int bb = mask_highest<W>(bm);
   int ba = mask_lowest<W>(am, L);
+  uint32_t bh = kNull16, ah = kNull16;
+  if (bb >= 0)
+    bh = (bid_ok && bb == bid_px) ? ((bword >> 16) == kNull16 ? bslot : (bword & kNull16))
+                                  : (bbw0 & kNull16);
+  if (ba < L)
+    ah = (ask_ok && ba == ask_px) ? ((aword >> 16) == kNull16 ? aslot : (aword & kNull16))
+                                  : (baw0 & kNull16);
+
+  // ---- match while the book is crossed (market.cu:145-274) ----
   int32_t fc = 0;
-  uint32_t emptied = 0;
-  int bhl = -1, ahl = -1;                         // level whose head slot is in bsl / asl
-  uint32_t bsl = kNull16, asl = kNull16;          // head slots of the best levels
-  uint32_t brs = 0xFFFFFFFFu, ars = 0xFFFFFFFFu;  // slots whose records are in brec / arec
+  uint32_t emptied = 0, forwarded = 0;
   uint4 brec = make_uint4(0, 0, 0, 0), arec = make_uint4(0, 0, 0, 0);
+  bool have_b = false, have_a = false;  // brec / arec hold the records of bh / ah
+  int pb = -1, pa = L;                  // levels whose words are read ahead in pbw / paw
+  uint32_t pbw = 0xFFFFFFFFu, paw = 0xFFFFFFFFu;
+  bool ahead = false;                   // read-ahead issued
 
   while (bb >= 0 && ba < L && bb >= ba) {
-    if (bhl != bb) {
-      bsl = lv[(size_t)bb * 4 + 0];
-      bhl = bb;
+    if (bh >= (uint32_t)O || ah >= (uint32_t)O) break;  // NULL head (:155)
+    // Records: before the first fill nothing has changed, so the inserted
+    // records come from registers; after that every size change has been
+    // written through, so memory is current.
+    if (!have_b) {
+      if (fc == 0 && bh == aslot) brec = kra;
+      else if (fc == 0 && bh == bslot) brec = krb;
+      else brec = rec[bh];
+      have_b = true;
     }
-    if (ahl != ba) {
-      asl = lv[(size_t)ba * 4 + 2];
-      ahl = ba;
+    if (!have_a) {
+      if (fc == 0 && ah == aslot) arec = kra;
+      else if (fc == 0 && ah == bslot) arec = krb;
+      else arec = rec[ah];
+      have_a = true;
     }
-    if (bsl >= (uint32_t)O || asl >= (uint32_t)O) break;  // NULL head (:155)
-    // A record is (re)loaded when its side's head slot changes. Every size
-    // change is written through to the record right away, so memory always
-    // holds the latest size, also for a slot cached on the other side.
-    if (brs != bsl) {
-      brec = rec[bsl];
-      brs = bsl;
-    }
-    if (ars != asl) {
-      arec = rec[asl];
-      ars = asl;
+    if (!ahead) {  // read the next level of each side ahead
+      uint64_t t[W];
+#pragma unroll
+      for (int i = 0; i < W; ++i) t[i] = bm[i];
+      mask_clear<W>(t, bb);
+      pb = mask_highest<W>(t);
+      if (pb >= 0) pbw = level_word(lv, pb, 0);
+#pragma unroll
+      for (int i = 0; i < W; ++i) t[i] = am[i];
+      mask_clear<W>(t, ba);
+      pa = mask_lowest<W>(t, L);
+      if (pa < L) paw = level_word(lv, pa, 1);
+      ahead = true;
     }
     const int32_t bsz = (int32_t)brec.x, asz = (int32_t)arec.x;
     const int32_t bcu = (int32_t)brec.y, acu = (int32_t)arec.y;
@@ -385,15 +497,32 @@ ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut
       fc = -1;
       break;
     }
-    const int64_t fi = m * (int64_t)F + fc;
-    out.prices[fi] = price;
-    out.sizes[fi] = qty;
-    out.taker[fi] = bid_quote ? acu : bcu;
-    out.quoter[fi] = bid_quote ? bcu : acu;
-    out.is_sell_quote[fi] = bid_quote ? 0 : 1;
-    out.quote_sizes[fi] = bid_quote ? bsz : asz;
-    out.tid[fi] = bid_quote ? atid : btid;
-    out.quote_tid[fi] = bid_quote ? btid : atid;
+    const int32_t row[8] = {price,
+                            qty,
+                            bid_quote ? acu : bcu,
+                            bid_quote ? bcu : acu,
+                            bid_quote ? 0 : 1,
+                            bid_quote ? bsz : asz,
+                            bid_quote ? atid : btid,
+                            bid_quote ? btid : atid};
+    if (bh == ah && bsz != 0) {
+      // One slot heads both sides with size s != 0: q = s, the slot becomes -s,
+      // neither side pops, and the next pass is the same with -s. The fills
+      // alternate s, -s until F; the trade is a self-trade (no portfolio
+      // change); the slot ends at s or -s by the parity of the fill count.
+      bulk.base = m * (int64_t)F + fc;
+      bulk.count = F - fc;
+      bulk.alt = 1;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) bulk.v[i] = row[i];
+      const int32_t s = ((F - fc) & 1) ? (int32_t)(0u - (uint32_t)bsz) : bsz;
+      reinterpret_cast<int32_t *>(rec + bh)[0] = s;
+      brec.x = arec.x = (uint32_t)s;
+      fc = -1;
+      if (STATS) ++forwarded;
+      break;
+    }
+    write_fill(out, m * (int64_t)F + fc, row);
     // (:221-232) A self-trade nets to zero, so it is skipped.
     if ((uint32_t)bcu < (uint32_t)C && (uint32_t)acu < (uint32_t)C && bcu != acu) {
       const uint32_t notional = (uint32_t)price * (uint32_t)qty;
@@ -404,41 +533,63 @@ ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut
     }
     ++fc;
     // (:237-238) both decrements land on one slot when bid and ask alias
-    if (bsl == asl) {
+    if (bh == ah) {
       const int32_t s = wsub(wsub(bsz, qty), qty);
       brec.x = arec.x = (uint32_t)s;
-      reinterpret_cast<int32_t *>(rec + bsl)[0] = s;
+      if (qty != 0) reinterpret_cast<int32_t *>(rec + bh)[0] = s;
     } else {
       brec.x = (uint32_t)wsub(bsz, qty);
       arec.x = (uint32_t)wsub(asz, qty);
-      reinterpret_cast<int32_t *>(rec + bsl)[0] = (int32_t)brec.x;
-      reinterpret_cast<int32_t *>(rec + asl)[0] = (int32_t)arec.x;
+      if (qty != 0) {
+        reinterpret_cast<int32_t *>(rec + bh)[0] = (int32_t)brec.x;
+        reinterpret_cast<int32_t *>(rec + ah)[0] = (int32_t)arec.x;
+      }
     }
+    const uint32_t bh_was = bh, ah_was = ah;
+    const int bb_was = bb, ba_was = ba;
     if (brec.x == 0u) {  // pop the bid head (:241-256)
-      const uint32_t nh = brec.w >> 16;
+      const uint32_t nh = rec_next(brec);
       if (nh == kNull16) {
-        *reinterpret_cast<uint32_t *>(lv + (size_t)bb * 4) = 0xFFFFFFFFu;
+        store_level_word(lv, bb, 0, 0xFFFFFFFFu);
         mask_clear<W>(bm, bb);
         if (STATS) ++emptied;
-        bb = mask_highest<W>(bm);
-        bhl = -1;
-      } else {
-        lv[(size_t)bb * 4] = (uint16_t)nh;
-        bsl = nh;
+        bb = mask_highest<W>(bm);  // the level read ahead
+        bh = bb >= 0 ? ((bb == pb ? pbw : level_word(lv, bb, 0)) & kNull16) : kNull16;
+        have_b = false;
+        ahead = false;
+      } else if (nh != bh) {
+        store_head(lv, bb, 0, nh);
+        bh = nh;
+        have_b = false;
       }
     }
     if (arec.x == 0u) {  // pop the ask head (:258-273)
-      const uint32_t nh = arec.w >> 16;
+      const uint32_t nh = rec_next(arec);
       if (nh == kNull16) {
-        *reinterpret_cast<uint32_t *>(lv + (size_t)ba * 4 + 2) = 0xFFFFFFFFu;
+        store_level_word(lv, ba, 1, 0xFFFFFFFFu);
         mask_clear<W>(am, ba);
         if (STATS) ++emptied;
         ba = mask_lowest<W>(am, L);
-        ahl = -1;
-      } else {
-        lv[(size_t)ba * 4 + 2] = (uint16_t)nh;
-        asl = nh;
+        ah = ba < L ? ((ba == pa ? paw : level_word(lv, ba, 1)) & kNull16) : kNull16;
+        have_a = false;
+        ahead = false;
+      } else if (nh != ah) {
+        store_head(lv, ba, 1, nh);
+        ah = nh;
+        have_a = false;
       }
+    }
+    if (qty == 0 && bh == bh_was && ah == ah_was && bb == bb_was && ba == ba_was) {
+      // Nothing changed (a size-0 head linked to itself): every further pass
+      // writes this same row until F. Portfolios and sizes are untouched.
+      bulk.base = m * (int64_t)F + fc;
+      bulk.count = F - fc;
+      bulk.alt = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) bulk.v[i] = row[i];
+      fc = -1;
+      if (STATS) ++forwarded;
+      break;
     }
   }
 
@@ -449,49 +600,44 @@ ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut
     b.masks[(int64_t)(W + i) * M + m] = am[i];
   }
   b.next_slot[m] = ns;
+
+  // ---- best bid / offer of the book as left (what get_bbo_kernel reads) ----
+  int32_t obs = 0, oas = 0;
+  if (bb >= 0 && bh < (uint32_t)O) {
+    if (have_b) obs = (int32_t)brec.x;
+    else if (fc == 0 && bh == aslot) obs = (int32_t)kra.x;
+    else if (fc == 0 && bh == bslot) obs = (int32_t)krb.x;
+    else obs = reinterpret_cast<const int32_t *>(rec + bh)[0];
+  }
+  if (ba < L && ah < (uint32_t)O) {
+    if (have_a) oas = (int32_t)arec.x;
+    else if (fc == 0 && ah == aslot) oas = (int32_t)kra.x;
+    else if (fc == 0 && ah == bslot) oas = (int32_t)krb.x;
+    else oas = reinterpret_cast<const int32_t *>(rec + ah)[0];
+  }
+  b.bbo[m] = (bb >= 0 && bh < (uint32_t)O) ? bb : ASTRA_NULL_INDEX;
+  b.bbo[M + m] = obs;
+  b.bbo[2 * M + m] = (ba < L && ah < (uint32_t)O) ? ba : ASTRA_NULL_INDEX;
+  b.bbo[3 * M + m] = oas;
+
   if (STATS) {  // uniform addresses: the compiler aggregates these per wave
     add_u64(b.stats + 0, (unsigned long long)(bid_ok + ask_ok));
     add_u64(b.stats + 1, (unsigned long long)(fc < 0 ? F : fc));
     add_u64(b.stats + 2, (unsigned long long)emptied);
     add_u64(b.stats + 3, (unsigned long long)(fc < 0));
+    add_u64(b.stats + 4, (unsigned long long)forwarded);
   }
 }
 
-// get_bbo_kernel (market.cu:280-320) for market m: best level from the masks,
-// size of that level's head order; an empty side is (NULL, 0).
-template <int W>
-ASTRA_HD void bbo_market(const Book &b, int32_t *bid_px, int32_t *bid_sz, int32_t *ask_px,
-                         int32_t *ask_sz, int64_t m) {
+// GetBBOs (market.cu:573-597) reads the cache the last call left: the best
+// level and the size of its head order per side, (NULL, 0) for an empty side.
+ASTRA_HD void bbo_copy_market(const Book &b, int32_t *bid_px, int32_t *bid_sz, int32_t *ask_px,
+                              int32_t *ask_sz, int64_t m) {
   const int64_t M = b.M;
-  uint64_t bm[W], am[W];
-#pragma unroll
-  for (int i = 0; i < W; ++i) {
-    bm[i] = b.masks[(int64_t)i * M + m];
-    am[i] = b.masks[(int64_t)(W + i) * M + m];
-  }
-  const uint16_t *lv = b.levels + m * (int64_t)b.L * 4;
-  const uint4 *rec = b.records + m * (int64_t)b.O;
-  const int bb = mask_highest<W>(bm);
-  const int ba = mask_lowest<W>(am, b.L);
-  int32_t obp = ASTRA_NULL_INDEX, obs = 0, oap = ASTRA_NULL_INDEX, oas = 0;
-  if (bb >= 0) {
-    const uint32_t h = lv[(size_t)bb * 4];
-    if (h < (uint32_t)b.O) {
-      obp = bb;
-      obs = reinterpret_cast<const int32_t *>(rec + h)[0];
-    }
-  }
-  if (ba < b.L) {
-    const uint32_t h = lv[(size_t)ba * 4 + 2];
-    if (h < (uint32_t)b.O) {
-      oap = ba;
-      oas = reinterpret_cast<const int32_t *>(rec + h)[0];
-    }
-  }
-  bid_px[m] = obp;
-  bid_sz[m] = obs;
-  ask_px[m] = oap;
-  ask_sz[m] = oas;
+  bid_px[m] = b.bbo[m];
+  bid_sz[m] = b.bbo[M + m];
+  ask_px[m] = b.bbo[2 * M + m];
+  ask_sz[m] = b.bbo[3 * M + m];
 }
 
 // update_last_prices_kernel (market.cu:767-786). A count above F (only possible
@@ -504,7 +650,8 @@ ASTRA_HD void last_price_market(int32_t *last, const int32_t *counts, const int3
 
 // ClearQuotes (market.cu:735-749) for thread t = (market, level): the level's
 // 8-byte word to all-NULL; the level-0 thread also zeroes the masks and the slot
-// counter. The reference also writes NULL into order_next; here a slot's next is
+// counter and empties the market's BBO cache. The reference also writes NULL
+// into order_next; here a slot's next is
 // overwritten whenever the slot is reused, and after the clear no list can
 // reach a slot that was not reused, so it is left alone (no observable
 // difference).
@@ -520,22 +667,58 @@ ASTRA_HD void clear_quotes_thread(const Book &b, const uint8_t *reset, int64_t t
 #pragma unroll
     for (int i = 0; i < 2 * W; ++i) b.masks[(int64_t)i * M + m] = 0ull;
     b.next_slot[m] = 0;
+    b.bbo[m] = ASTRA_NULL_INDEX;
+    b.bbo[M + m] = 0;
+    b.bbo[2 * M + m] = ASTRA_NULL_INDEX;
+    b.bbo[3 * M + m] = 0;
   }
 }
 
 // ---- __global__ wrappers ----
 
+// Writes the rows owed by fast-forwarded markets of this wavefront: each such
+// lane's rows are written by all 64 lanes together, coalesced.
+__device__ __forceinline__ void write_bulk_wave(const FillOut &out, const Bulk &bk) {
+  uint64_t pending = __ballot(bk.count > 0);
+  const int lane = (int)__lane_id();
+  while (pending) {
+    const int src = __ffsll((unsigned long long)pending) - 1;
+    pending &= pending - 1;
+    const int32_t base_lo = __shfl((int32_t)(uint32_t)bk.base, src);
+    const int32_t base_hi = __shfl((int32_t)(bk.base >> 32), src);
+    const int64_t base = (int64_t)(((uint64_t)(uint32_t)base_hi << 32) | (uint32_t)base_lo);
+    const int32_t count = __shfl(bk.count, src);
+    const int32_t alt = __shfl(bk.alt, src);
+    int32_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __shfl(bk.v[i], src);
+    for (int32_t k = lane; k < count; k += 64) {
+      int32_t r[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] = v[i];
+      if (alt && (k & 1)) {
+        r[1] = (int32_t)(0u - (uint32_t)r[1]);
+        r[5] = (int32_t)(0u - (uint32_t)r[5]);
+      }
+      write_fill(out, base + k, r);
+    }
+  }
+}
+
+// All 64 lanes of a wavefront reach write_bulk_wave (no early return).
 template <int W, bool STATS>
 __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, FillOut out) {
   const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (m < b.M) quote_match_market<W, STATS>(b, in, out, m);
+  Bulk bulk;
+  bulk.count = 0;
+  if (m < b.M) quote_match_market<W, STATS>(b, in, out, m, bulk);
+  write_bulk_wave(out, bulk);
 }
 
-template <int W>
 __global__ __launch_bounds__(256) void bbo_kernel(Book b, int32_t *bid_px, int32_t *bid_sz,
-                                                   int32_t *ask_px, int32_t *ask_sz) {
+                                                  int32_t *ask_px, int32_t *ask_sz) {
   const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (m < b.M) bbo_market<W>(b, bid_px, bid_sz, ask_px, ask_sz, m);
+  if (m < b.M) bbo_copy_market(b, bid_px, bid_sz, ask_px, ask_sz, m);
 }
 
 __global__ __launch_bounds__(256) void last_price_kernel(int32_t *last, const int32_t *counts,
@@ -577,10 +760,13 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
 #ifdef ASTRA_HOST_EMULATION
   (void)s;
   for (int64_t m = 0; m < b.M; ++m) {
+    Bulk bulk;
+    bulk.count = 0;
     if (b.stats)
-      quote_match_market<W, true>(b, in, fo, m);
+      quote_match_market<W, true>(b, in, fo, m, bulk);
     else
-      quote_match_market<W, false>(b, in, fo, m);
+      quote_match_market<W, false>(b, in, fo, m, bulk);
+    if (bulk.count > 0) write_bulk_host(fo, bulk);
   }
 #else
   if (b.stats)
@@ -594,16 +780,14 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   return ASTRA_OK;
 }
 
-template <int W>
 int launch_bbo(const astra_market *h, int32_t *bp, int32_t *bs, int32_t *ap, int32_t *as,
                hipStream_t s) {
   const Book b = book_of(h);
 #ifdef ASTRA_HOST_EMULATION
   (void)s;
-  for (int64_t m = 0; m < b.M; ++m) bbo_market<W>(b, bp, bs, ap, as, m);
+  for (int64_t m = 0; m < b.M; ++m) bbo_copy_market(b, bp, bs, ap, as, m);
 #else
-  hipLaunchKernelGGL((bbo_kernel<W>), dim3(grid_for(b.M, h->block)), dim3(h->block), 0, s, b,
-                     bp, bs, ap, as);
+  hipLaunchKernelGGL(bbo_kernel, dim3(grid_for(b.M, 256)), dim3(256), 0, s, b, bp, bs, ap, as);
 #endif
   ASTRA_HIP_CHECK(rt_last_error(), "GetBBOs");
   return ASTRA_OK;
@@ -663,13 +847,20 @@ int launch_last_price(int32_t *last, const int32_t *counts, const int32_t *price
   return ASTRA_OK;
 }
 
-// Empty book: masks 0, slot counters 0, level words NULL, portfolios 0 (the
+// Empty book: masks 0, slot counters 0, BBO cache empty, level words NULL,
+// portfolios 0 (the
 // order records are left alone: no list reaches a slot before it is written).
 int init_book(astra_market *h, hipStream_t s) {
   const Layout &l = h->lay;
   int rc;
-  if ((rc = launch_fill(h->ws + l.masks, (int64_t)(l.levels - l.masks) / 4, 0u, s, "init")))
+  if ((rc = launch_fill(h->ws + l.masks, (int64_t)(l.bbo - l.masks) / 4, 0u, s, "init")))
     return rc;
+  // BBO cache of an empty book: (NULL, 0, NULL, 0)
+  int32_t *bbo = reinterpret_cast<int32_t *>(h->ws + l.bbo);
+  if ((rc = launch_fill(bbo, h->M, 0xFFFFFFFFu, s, "init"))) return rc;
+  if ((rc = launch_fill(bbo + h->M, h->M, 0u, s, "init"))) return rc;
+  if ((rc = launch_fill(bbo + 2 * (int64_t)h->M, h->M, 0xFFFFFFFFu, s, "init"))) return rc;
+  if ((rc = launch_fill(bbo + 3 * (int64_t)h->M, h->M, 0u, s, "init"))) return rc;
   if ((rc = launch_fill(h->ws + l.levels, (int64_t)h->M * h->L * 2, 0xFFFFFFFFu, s, "init")))
     return rc;
   return launch_fill(h->ws + l.portfolios, (int64_t)h->M * h->C * 2, 0u, s, "init");
@@ -846,7 +1037,7 @@ int astra_market_get_bbos(const astra_market *h, int32_t *bid_px, int32_t *bid_s
   if (!bid_px || !bid_sz || !ask_px || !ask_sz)
     return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL BBO pointer");
   DeviceGuard g(h->device);
-  ASTRA_DISPATCH_W(h->lay.W, launch_bbo, h, bid_px, bid_sz, ask_px, ask_sz, as_stream(stream));
+  return launch_bbo(h, bid_px, bid_sz, ask_px, ask_sz, as_stream(stream));
 }
 
 int astra_update_last_prices(int32_t *last, const int32_t *counts, const int32_t *prices,

@@ -172,12 +172,12 @@ def main():
     bbo_ms = np.array([e[1].elapsed_time(e[2]) for e in evs]) if bbo else np.zeros(K)
 
     # ---- D: exact work counts for the algorithmic bytes ----
-    counters = torch.zeros(4, dtype=torch.int64, device=dev)
+    counters = torch.zeros(8, dtype=torch.int64, device=dev)
     snaps[2]._set_stats(counters)
     for t in range(W, T):
         snaps[2].add_two_sided_quotes(*rows[t], fills)
     torch.cuda.synchronize()
-    n_ins, n_fill, n_empty, n_ovf = (int(x) for x in counters.cpu().tolist())
+    n_ins, n_fill, n_empty, n_ovf, n_ff = (int(x) for x in counters.cpu().tolist()[:5])
     snaps[2]._set_stats(None)
     log(f"work over {K} steps: inserts {n_ins}, fill rows {n_fill}, emptied {n_empty}, overflow {n_ovf}")
 

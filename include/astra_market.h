@@ -94,7 +94,9 @@ int astra_market_add_two_sided_quotes(astra_market *market, const int32_t *bid_p
                                       int32_t *fill_tid, int32_t *fill_quote_tid,
                                       int32_t *fill_counts, void *stream);
 
-/* VecMarket::GetBBOs (market.cu:573-597): four int32 [M] outputs. */
+/* VecMarket::GetBBOs (market.cu:573-597): four int32 [M] outputs. The values
+ * are those of the book as the last mutating call left it (the matching kernel
+ * computes them; this call copies them out). */
 int astra_market_get_bbos(const astra_market *market, int32_t *best_bid_prices,
                           int32_t *best_bid_sizes, int32_t *best_ask_prices,
                           int32_t *best_ask_sizes, void *stream);
@@ -126,12 +128,13 @@ int astra_market_portfolios(const astra_market *market, int32_t **portfolios);
 int astra_market_to_string(const astra_market *market, int32_t market_id, char *buf,
                            size_t buflen, size_t *needed, void *stream);
 
-/* Diagnostic, no counterpart in the reference: while `counters` (int64 [4],
+/* Diagnostic, no counterpart in the reference: while `counters` (int64 [8],
  * device memory, caller-zeroed) is set, astra_market_add_two_sided_quotes also
- * adds to it the accepted order inserts, fill rows written (F for a market that
- * overflowed), price levels emptied and markets that overflowed. These are the
- * work counts of the algorithmic-byte roofline. NULL switches it off (the
- * default); the timed path never has it on. */
+ * adds to [0..4] the accepted order inserts, fill rows written (F for a market
+ * that overflowed), price levels emptied, markets that overflowed, and
+ * overflows reached by fast-forwarding a repeating loop state ([5..7] unused).
+ * These are the work counts of the algorithmic-byte roofline. NULL switches it
+ * off (the default); the timed path never has it on. */
 int astra_market_set_stats(astra_market *market, int64_t *counters);
 
 /* Host TID counter (market.h:338): read, and set (for restoring a snapshot). */
