@@ -173,6 +173,7 @@ struct astra_market {
   int32_t flags;
   int32_t tid;                // host TID counter, market.h:338
   int block;                  // launch block size of the per-market kernels
+  int32_t stage_budget;       // loop passes before a market is staged in LDS (0: never)
   unsigned long long *stats;  // see astra_market_set_stats
   char *ws;
   size_t ws_bytes;
@@ -343,47 +344,197 @@ inline void write_bulk_host(const FillOut &out, const Bulk &bk) {
   }
 }
 
-// add_orders_kernel + match_orders_kernel (market.cu:17-100, 102-278) for
-// market m, followed by the best bid/offer of the resulting book (what
-// get_bbo_kernel, market.cu:280-320, would read), which is left in the
-// workspace's BBO cache. STATS builds the diagnostic variant that also counts
-// inserts, fill rows, emptied levels, overflowed markets and fast-forwards.
+// Portfolio update of one fill row (market.cu:221-232): the buyer is the bid
+// side's customer, i.e. the taker when the ask quotes and the quoter otherwise.
+// A self-trade nets to zero, so it is skipped.
+ASTRA_HD void apply_portfolio(int32_t *pf, int32_t C, int32_t price, int32_t qty, int32_t taker,
+                              int32_t quoter, bool ask_quotes) {
+  const int32_t buyer = ask_quotes ? taker : quoter, seller = ask_quotes ? quoter : taker;
+  if ((uint32_t)buyer < (uint32_t)C && (uint32_t)seller < (uint32_t)C && buyer != seller) {
+    const uint32_t notional = (uint32_t)price * (uint32_t)qty;
+    add_i32(pf + 2 * buyer, qty);
+    add_i32(pf + 2 * buyer + 1, (int32_t)(0u - notional));
+    add_i32(pf + 2 * seller, (int32_t)(0u - (uint32_t)qty));
+    add_i32(pf + 2 * seller + 1, (int32_t)notional);
+  }
+}
+
+// Fill rows a lane has produced but not yet written. On the GPU the rows live
+// in LDS as [field][row][lane] (a row write by 64 lanes touches 64 consecutive
+// words: no bank conflicts); the host build keeps them in a local array. Rows
+// go out kRows at a time as aligned vector stores (rows k..k+kRows-1 of one
+// market are contiguous in each field array), together with the portfolio
+// updates they imply. In direct mode (used once the LDS holds a staged book)
+// each row is written as it comes. Nothing beyond the call's last row is ever
+// written: the reference leaves later entries of a FillBatch untouched.
+constexpr int kRows = 4;
+
+struct FillSink {
+#if defined(__HIP_DEVICE_COMPILE__)
+  int32_t *lds;  // this wavefront's [8][kRows][64] buffer
+  int lane;
+  __device__ int32_t &at(int f, int r) const { return lds[(f * kRows + r) * 64 + lane]; }
+#else
+  mutable int32_t buf[8][kRows];
+  int32_t &at(int f, int r) const { return buf[f][r]; }
+#endif
+  int64_t base = 0;  // fill index of buffered row 0
+  int32_t n = 0;     // rows buffered
+  bool direct = false;
+
+  ASTRA_HD void flush(const FillOut &out, int32_t *pf, int32_t C) {
+    if (n == 0) return;
+    int32_t *dst32[7] = {out.prices, out.sizes, out.taker, out.quoter, out.quote_sizes, out.tid,
+                         out.quote_tid};
+    const int fidx[7] = {0, 1, 2, 3, 5, 6, 7};
+#pragma unroll
+    for (int j = 0; j < 7; ++j) {
+      int32_t *d = dst32[j] + base;
+      const int f = fidx[j];
+      if ((reinterpret_cast<uintptr_t>(d) & 15) == 0) {
+        if (n == 4) {
+          *reinterpret_cast<int4 *>(d) = make_int4(at(f, 0), at(f, 1), at(f, 2), at(f, 3));
+        } else {
+          if (n & 2) *reinterpret_cast<int2 *>(d) = make_int2(at(f, 0), at(f, 1));
+          if (n & 1) d[n - 1] = at(f, n - 1);
+        }
+      } else {
+        for (int r = 0; r < n; ++r) d[r] = at(f, r);
+      }
+    }
+    uint8_t *d8 = out.is_sell_quote + base;
+    if ((reinterpret_cast<uintptr_t>(d8) & 3) == 0) {
+      if (n == 4) {
+        *reinterpret_cast<uint32_t *>(d8) = (uint32_t)at(4, 0) | ((uint32_t)at(4, 1) << 8) |
+                                            ((uint32_t)at(4, 2) << 16) | ((uint32_t)at(4, 3) << 24);
+      } else {
+        if (n & 2)
+          *reinterpret_cast<uint16_t *>(d8) =
+              (uint16_t)((uint32_t)at(4, 0) | ((uint32_t)at(4, 1) << 8));
+        if (n & 1) d8[n - 1] = (uint8_t)at(4, n - 1);
+      }
+    } else {
+      for (int r = 0; r < n; ++r) d8[r] = (uint8_t)at(4, r);
+    }
+    for (int r = 0; r < n; ++r)
+      apply_portfolio(pf, C, at(0, r), at(1, r), at(2, r), at(3, r), at(4, r) != 0);
+    base += n;
+    n = 0;
+  }
+
+  ASTRA_HD void put(const FillOut &out, int32_t *pf, int32_t C, const int32_t (&row)[8]) {
+    if (direct) {
+      write_fill(out, base++, row);
+      apply_portfolio(pf, C, row[0], row[1], row[2], row[3], row[4] != 0);
+      return;
+    }
+#pragma unroll
+    for (int f = 0; f < 8; ++f) at(f, n) = row[f];
+    if (++n == kRows) flush(out, pf, C);
+  }
+};
+
+// What stays fixed for a market during its matching loop.
+struct MarketCtx {
+  int64_t m;
+  int32_t L, O, F, C;
+  uint16_t *lv;  // the market's level words and order records in global memory
+  uint4 *rec;
+  int32_t *pf;
+  uint32_t bslot, aslot;  // slots the two inserts took (0xFFFFFFFF if none)
+  uint4 krb, kra;         // their records as stored, next fields included
+  int32_t ns;             // ring position after the inserts
+  bool bid_ok, ask_ok;
+};
+
+// The matching loop's state: everything a lane needs to resume the loop later.
+template <int W>
+struct LoopState {
+  uint64_t bm[W], am[W];
+  int bb, ba;                  // best levels
+  uint32_t bh, ah;             // their head slots
+  uint4 brec, arec;            // records of bh / ah when have_b / have_a
+  bool have_b, have_a;
+  int pb, pa;                  // next levels whose words were read ahead
+  uint32_t pbw, paw;
+  bool ahead;                  // read-ahead issued for the current levels
+  int32_t fc;                  // fills so far (-1 after an overflow)
+  uint32_t emptied, forwarded; // diagnostic counts
+};
+
+// The book as the loop sees it. GlobalBook: the market's arrays in global
+// memory. StagedBook: reads from a copy of the market's records and level
+// words (in LDS on the GPU) and writes to both copies, so global memory stays
+// current.
+struct GlobalBook {
+  uint16_t *lv;
+  uint4 *rec;
+  ASTRA_HD uint4 record(uint32_t s) const { return rec[s]; }
+  ASTRA_HD uint32_t word(int32_t p, int side) const { return level_word(lv, p, side); }
+  ASTRA_HD void set_size(uint32_t s, int32_t v) const {
+    reinterpret_cast<int32_t *>(rec + s)[0] = v;
+  }
+  ASTRA_HD void set_word(int32_t p, int side, uint32_t w) const { store_level_word(lv, p, side, w); }
+  ASTRA_HD void set_head(int32_t p, int side, uint32_t h) const { store_head(lv, p, side, h); }
+};
+
+struct StagedBook {
+  uint16_t *lv;
+  uint4 *rec;
+  uint16_t *slv;
+  uint4 *srec;
+  ASTRA_HD uint4 record(uint32_t s) const { return srec[s]; }
+  ASTRA_HD uint32_t word(int32_t p, int side) const { return level_word(slv, p, side); }
+  ASTRA_HD void set_size(uint32_t s, int32_t v) const {
+    reinterpret_cast<int32_t *>(srec + s)[0] = v;
+    reinterpret_cast<int32_t *>(rec + s)[0] = v;
+  }
+  ASTRA_HD void set_word(int32_t p, int side, uint32_t w) const {
+    store_level_word(slv, p, side, w);
+    store_level_word(lv, p, side, w);
+  }
+  ASTRA_HD void set_head(int32_t p, int side, uint32_t h) const {
+    store_head(slv, p, side, h);
+    store_head(lv, p, side, h);
+  }
+};
+
+// add_orders_kernel (market.cu:17-100) for market m and the set-up of the
+// matching loop: masks, the inserts, and the heads of the best levels.
 //
-// Memory round trips are what a lane waits on, so: the two insert levels and
-// the two current best levels are read in one round trip, heads at loop entry
-// come from those words, the records just inserted come from registers, and the
-// next level of each side is read ahead while the current one is consumed.
-//
-// Two loop states repeat forever (both arise from ring-slot reuse): a size-0
-// head that links to itself (each pass emits the same zero-size fill and
-// changes nothing) and one slot heading both sides with size s != 0 (fills of
-// s and -s alternate). The reference loops until F fills and then writes -1;
-// here the owed rows are handed to the caller in `bulk`, the final state is set
-// directly, and the count is -1, which is the same result.
-template <int W, bool STATS>
-ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut &out, int64_t m,
-                                 Bulk &bulk) {
+// Memory round trips are what a lane waits on, so the two insert levels and
+// the two current best levels are read in one round trip, and the heads at
+// loop entry come from those words.
+template <int W>
+ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, MarketCtx &c,
+                             LoopState<W> &s) {
   const int64_t M = b.M;
-  const int32_t L = b.L, O = b.O, F = b.F, C = b.C;
+  const int32_t L = b.L, O = b.O;
+  c.m = m;
+  c.L = L;
+  c.O = O;
+  c.F = b.F;
+  c.C = b.C;
+  c.lv = b.levels + m * (int64_t)L * 4;
+  c.rec = b.records + m * (int64_t)O;
+  c.pf = b.portfolios + m * (int64_t)b.C * 2;
+  uint16_t *lv = c.lv;
+  uint4 *rec = c.rec;
 
   const int32_t bid_px = in.bid_px[m], bid_sz = in.bid_sz[m];
   const int32_t ask_px = in.ask_px[m], ask_sz = in.ask_sz[m];
   const int32_t cust = in.cust[m];
-  uint64_t bm[W], am[W];
 #pragma unroll
   for (int i = 0; i < W; ++i) {
-    bm[i] = b.masks[(int64_t)i * M + m];
-    am[i] = b.masks[(int64_t)(W + i) * M + m];
+    s.bm[i] = b.masks[(int64_t)i * M + m];
+    s.am[i] = b.masks[(int64_t)(W + i) * M + m];
   }
   int32_t ns = b.next_slot[m];
-  uint16_t *lv = b.levels + m * (int64_t)L * 4;
-  uint4 *rec = b.records + m * (int64_t)O;
-  int32_t *pf = b.portfolios + m * (int64_t)C * 2;
 
   const bool bid_ok = bid_sz > 0 && (uint32_t)bid_px < (uint32_t)L;
   const bool ask_ok = ask_sz > 0 && (uint32_t)ask_px < (uint32_t)L;
-  const int bb0 = mask_highest<W>(bm);
-  const int ba0 = mask_lowest<W>(am, L);
+  const int bb0 = mask_highest<W>(s.bm);
+  const int ba0 = mask_lowest<W>(s.am, L);
   // One round trip for the four level words this call may start from. The bid
   // insert only writes bid halves of level words, so the ask words read here
   // are the ones the ask insert would have read after it.
@@ -406,7 +557,7 @@ ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut
     const uint32_t old_tail = bword >> 16;
     if (old_tail == kNull16) {
       store_level_word(lv, bid_px, 0, bslot | (bslot << 16));
-      mask_set<W>(bm, bid_px);
+      mask_set<W>(s.bm, bid_px);
     } else {
       lv[(size_t)bid_px * 4 + 1] = (uint16_t)bslot;
       if (old_tail < (uint32_t)O) {
@@ -425,7 +576,7 @@ ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut
     const uint32_t old_tail = aword >> 16;
     if (old_tail == kNull16) {
       store_level_word(lv, ask_px, 1, aslot | (aslot << 16));
-      mask_set<W>(am, ask_px);
+      mask_set<W>(s.am, ask_px);
     } else {
       lv[(size_t)ask_px * 4 + 3] = (uint16_t)aslot;
       if (old_tail < (uint32_t)O) {
@@ -435,66 +586,91 @@ ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut
       }
     }
   }
+  c.bslot = bslot;
+  c.aslot = aslot;
+  c.krb = krb;
+  c.kra = kra;
+  c.ns = ns;
+  c.bid_ok = bid_ok;
+  c.ask_ok = ask_ok;
 
   // ---- heads of the best levels, known without another read ----
-  int bb = mask_highest<W>(bm);
-  int ba = mask_lowest<W>(am, L);
-  uint32_t bh = kNull16, ah = kNull16;
-  if (bb >= 0)
-    bh = (bid_ok && bb == bid_px) ? ((bword >> 16) == kNull16 ? bslot : (bword & kNull16))
-                                  : (bbw0 & kNull16);
-  if (ba < L)
-    ah = (ask_ok && ba == ask_px) ? ((aword >> 16) == kNull16 ? aslot : (aword & kNull16))
-                                  : (baw0 & kNull16);
+  s.bb = mask_highest<W>(s.bm);
+  s.ba = mask_lowest<W>(s.am, L);
+  s.bh = kNull16;
+  s.ah = kNull16;
+  if (s.bb >= 0)
+    s.bh = (bid_ok && s.bb == bid_px) ? ((bword >> 16) == kNull16 ? bslot : (bword & kNull16))
+                                      : (bbw0 & kNull16);
+  if (s.ba < L)
+    s.ah = (ask_ok && s.ba == ask_px) ? ((aword >> 16) == kNull16 ? aslot : (aword & kNull16))
+                                      : (baw0 & kNull16);
+  s.brec = make_uint4(0, 0, 0, 0);
+  s.arec = make_uint4(0, 0, 0, 0);
+  s.have_b = s.have_a = false;
+  s.pb = -1;
+  s.pa = L;
+  s.pbw = s.paw = 0xFFFFFFFFu;
+  s.ahead = false;
+  s.fc = 0;
+  s.emptied = s.forwarded = 0;
+}
 
-  // ---- match while the book is crossed (market.cu:145-274) ----
-  int32_t fc = 0;
-  uint32_t emptied = 0, forwarded = 0;
-  uint4 brec = make_uint4(0, 0, 0, 0), arec = make_uint4(0, 0, 0, 0);
-  bool have_b = false, have_a = false;  // brec / arec hold the records of bh / ah
-  int pb = -1, pa = L;                  // levels whose words are read ahead in pbw / paw
-  uint32_t pbw = 0xFFFFFFFFu, paw = 0xFFFFFFFFu;
-  bool ahead = false;                   // read-ahead issued
-
-  while (bb >= 0 && ba < L && bb >= ba) {
-    if (bh >= (uint32_t)O || ah >= (uint32_t)O) break;  // NULL head (:155)
+// match_orders_kernel's crossing loop (market.cu:145-274). Runs at most
+// `budget` passes; returns false (state intact, nothing of the next pass done)
+// when the budget ran out first.
+//
+// Two loop states repeat forever (both arise from ring-slot reuse): a size-0
+// head that links to itself (each pass emits the same zero-size fill and
+// changes nothing) and one slot heading both sides with size s != 0 (fills of
+// s and -s alternate). The reference loops until F fills and then writes -1;
+// here the owed rows are handed to the caller in `bulk`, the final state is set
+// directly, and the count is -1, which is the same result.
+template <int W, bool STATS, class BookMem>
+ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, FillSink &sink,
+                         const FillOut &out, Bulk &bulk, int32_t budget) {
+  const int32_t L = c.L, O = c.O, F = c.F;
+  int32_t passes = 0;
+  while (s.bb >= 0 && s.ba < L && s.bb >= s.ba) {
+    if (s.bh >= (uint32_t)O || s.ah >= (uint32_t)O) break;  // NULL head (:155)
+    if (passes++ >= budget) return false;
     // Records: before the first fill nothing has changed, so the inserted
     // records come from registers; after that every size change has been
     // written through, so memory is current.
-    if (!have_b) {
-      if (fc == 0 && bh == aslot) brec = kra;
-      else if (fc == 0 && bh == bslot) brec = krb;
-      else brec = rec[bh];
-      have_b = true;
+    if (!s.have_b) {
+      if (s.fc == 0 && s.bh == c.aslot) s.brec = c.kra;
+      else if (s.fc == 0 && s.bh == c.bslot) s.brec = c.krb;
+      else s.brec = bk.record(s.bh);
+      s.have_b = true;
     }
-    if (!have_a) {
-      if (fc == 0 && ah == aslot) arec = kra;
-      else if (fc == 0 && ah == bslot) arec = krb;
-      else arec = rec[ah];
-      have_a = true;
+    if (!s.have_a) {
+      if (s.fc == 0 && s.ah == c.aslot) s.arec = c.kra;
+      else if (s.fc == 0 && s.ah == c.bslot) s.arec = c.krb;
+      else s.arec = bk.record(s.ah);
+      s.have_a = true;
     }
-    if (!ahead) {  // read the next level of each side ahead
+    if (!s.ahead) {  // read the next level of each side ahead
       uint64_t t[W];
 #pragma unroll
-      for (int i = 0; i < W; ++i) t[i] = bm[i];
-      mask_clear<W>(t, bb);
-      pb = mask_highest<W>(t);
-      if (pb >= 0) pbw = level_word(lv, pb, 0);
+      for (int i = 0; i < W; ++i) t[i] = s.bm[i];
+      mask_clear<W>(t, s.bb);
+      s.pb = mask_highest<W>(t);
+      if (s.pb >= 0) s.pbw = bk.word(s.pb, 0);
 #pragma unroll
-      for (int i = 0; i < W; ++i) t[i] = am[i];
-      mask_clear<W>(t, ba);
-      pa = mask_lowest<W>(t, L);
-      if (pa < L) paw = level_word(lv, pa, 1);
-      ahead = true;
+      for (int i = 0; i < W; ++i) t[i] = s.am[i];
+      mask_clear<W>(t, s.ba);
+      s.pa = mask_lowest<W>(t, L);
+      if (s.pa < L) s.paw = bk.word(s.pa, 1);
+      s.ahead = true;
     }
-    const int32_t bsz = (int32_t)brec.x, asz = (int32_t)arec.x;
-    const int32_t bcu = (int32_t)brec.y, acu = (int32_t)arec.y;
-    const int32_t btid = (int32_t)brec.z, atid = (int32_t)arec.z;
+    const int32_t bsz = (int32_t)s.brec.x, asz = (int32_t)s.arec.x;
+    const int32_t bcu = (int32_t)s.brec.y, acu = (int32_t)s.arec.y;
+    const int32_t btid = (int32_t)s.brec.z, atid = (int32_t)s.arec.z;
     const bool bid_quote = btid < atid;  // earlier TID rests (:172)
-    const int32_t price = (int32_t)((bid_quote ? brec.w : arec.w) & kNull16);
+    const int32_t price = (int32_t)((bid_quote ? s.brec.w : s.arec.w) & kNull16);
     const int32_t qty = bsz < asz ? bsz : asz;
-    if (fc >= F) {  // overflow sentinel (:187-195)
-      fc = -1;
+    if (s.fc >= F) {  // overflow sentinel (:187-195)
+      s.fc = -1;
       break;
     }
     const int32_t row[8] = {price,
@@ -505,127 +681,130 @@ ASTRA_HD void quote_match_market(const Book &b, const QuoteIn &in, const FillOut
                             bid_quote ? bsz : asz,
                             bid_quote ? atid : btid,
                             bid_quote ? btid : atid};
-    if (bh == ah && bsz != 0) {
+    if (s.bh == s.ah && bsz != 0) {
       // One slot heads both sides with size s != 0: q = s, the slot becomes -s,
       // neither side pops, and the next pass is the same with -s. The fills
       // alternate s, -s until F; the trade is a self-trade (no portfolio
       // change); the slot ends at s or -s by the parity of the fill count.
-      bulk.base = m * (int64_t)F + fc;
-      bulk.count = F - fc;
+      bulk.base = c.m * (int64_t)F + s.fc;
+      bulk.count = F - s.fc;
       bulk.alt = 1;
 #pragma unroll
       for (int i = 0; i < 8; ++i) bulk.v[i] = row[i];
-      const int32_t s = ((F - fc) & 1) ? (int32_t)(0u - (uint32_t)bsz) : bsz;
-      reinterpret_cast<int32_t *>(rec + bh)[0] = s;
-      brec.x = arec.x = (uint32_t)s;
-      fc = -1;
-      if (STATS) ++forwarded;
+      const int32_t fin = ((F - s.fc) & 1) ? (int32_t)(0u - (uint32_t)bsz) : bsz;
+      bk.set_size(s.bh, fin);
+      s.brec.x = s.arec.x = (uint32_t)fin;
+      s.fc = -1;
+      if (STATS) ++s.forwarded;
       break;
     }
-    write_fill(out, m * (int64_t)F + fc, row);
-    // (:221-232) A self-trade nets to zero, so it is skipped.
-    if ((uint32_t)bcu < (uint32_t)C && (uint32_t)acu < (uint32_t)C && bcu != acu) {
-      const uint32_t notional = (uint32_t)price * (uint32_t)qty;
-      add_i32(pf + 2 * bcu, qty);
-      add_i32(pf + 2 * bcu + 1, (int32_t)(0u - notional));
-      add_i32(pf + 2 * acu, (int32_t)(0u - (uint32_t)qty));
-      add_i32(pf + 2 * acu + 1, (int32_t)notional);
-    }
-    ++fc;
+    sink.put(out, c.pf, c.C, row);  // the row and its portfolio update (:198-232)
+    ++s.fc;
     // (:237-238) both decrements land on one slot when bid and ask alias
-    if (bh == ah) {
-      const int32_t s = wsub(wsub(bsz, qty), qty);
-      brec.x = arec.x = (uint32_t)s;
-      if (qty != 0) reinterpret_cast<int32_t *>(rec + bh)[0] = s;
+    if (s.bh == s.ah) {
+      const int32_t sz = wsub(wsub(bsz, qty), qty);
+      s.brec.x = s.arec.x = (uint32_t)sz;
+      if (qty != 0) bk.set_size(s.bh, sz);
     } else {
-      brec.x = (uint32_t)wsub(bsz, qty);
-      arec.x = (uint32_t)wsub(asz, qty);
+      s.brec.x = (uint32_t)wsub(bsz, qty);
+      s.arec.x = (uint32_t)wsub(asz, qty);
       if (qty != 0) {
-        reinterpret_cast<int32_t *>(rec + bh)[0] = (int32_t)brec.x;
-        reinterpret_cast<int32_t *>(rec + ah)[0] = (int32_t)arec.x;
+        bk.set_size(s.bh, (int32_t)s.brec.x);
+        bk.set_size(s.ah, (int32_t)s.arec.x);
       }
     }
-    const uint32_t bh_was = bh, ah_was = ah;
-    const int bb_was = bb, ba_was = ba;
-    if (brec.x == 0u) {  // pop the bid head (:241-256)
-      const uint32_t nh = rec_next(brec);
+    const uint32_t bh_was = s.bh, ah_was = s.ah;
+    const int bb_was = s.bb, ba_was = s.ba;
+    if (s.brec.x == 0u) {  // pop the bid head (:241-256)
+      const uint32_t nh = rec_next(s.brec);
       if (nh == kNull16) {
-        store_level_word(lv, bb, 0, 0xFFFFFFFFu);
-        mask_clear<W>(bm, bb);
-        if (STATS) ++emptied;
-        bb = mask_highest<W>(bm);  // the level read ahead
-        bh = bb >= 0 ? ((bb == pb ? pbw : level_word(lv, bb, 0)) & kNull16) : kNull16;
-        have_b = false;
-        ahead = false;
-      } else if (nh != bh) {
-        store_head(lv, bb, 0, nh);
-        bh = nh;
-        have_b = false;
+        bk.set_word(s.bb, 0, 0xFFFFFFFFu);
+        mask_clear<W>(s.bm, s.bb);
+        if (STATS) ++s.emptied;
+        s.bb = mask_highest<W>(s.bm);  // the level read ahead
+        s.bh = s.bb >= 0 ? ((s.bb == s.pb ? s.pbw : bk.word(s.bb, 0)) & kNull16) : kNull16;
+        s.have_b = false;
+        s.ahead = false;
+      } else if (nh != s.bh) {
+        bk.set_head(s.bb, 0, nh);
+        s.bh = nh;
+        s.have_b = false;
       }
     }
-    if (arec.x == 0u) {  // pop the ask head (:258-273)
-      const uint32_t nh = rec_next(arec);
+    if (s.arec.x == 0u) {  // pop the ask head (:258-273)
+      const uint32_t nh = rec_next(s.arec);
       if (nh == kNull16) {
-        store_level_word(lv, ba, 1, 0xFFFFFFFFu);
-        mask_clear<W>(am, ba);
-        if (STATS) ++emptied;
-        ba = mask_lowest<W>(am, L);
-        ah = ba < L ? ((ba == pa ? paw : level_word(lv, ba, 1)) & kNull16) : kNull16;
-        have_a = false;
-        ahead = false;
-      } else if (nh != ah) {
-        store_head(lv, ba, 1, nh);
-        ah = nh;
-        have_a = false;
+        bk.set_word(s.ba, 1, 0xFFFFFFFFu);
+        mask_clear<W>(s.am, s.ba);
+        if (STATS) ++s.emptied;
+        s.ba = mask_lowest<W>(s.am, L);
+        s.ah = s.ba < L ? ((s.ba == s.pa ? s.paw : bk.word(s.ba, 1)) & kNull16) : kNull16;
+        s.have_a = false;
+        s.ahead = false;
+      } else if (nh != s.ah) {
+        bk.set_head(s.ba, 1, nh);
+        s.ah = nh;
+        s.have_a = false;
       }
     }
-    if (qty == 0 && bh == bh_was && ah == ah_was && bb == bb_was && ba == ba_was) {
+    if (qty == 0 && s.bh == bh_was && s.ah == ah_was && s.bb == bb_was && s.ba == ba_was) {
       // Nothing changed (a size-0 head linked to itself): every further pass
       // writes this same row until F. Portfolios and sizes are untouched.
-      bulk.base = m * (int64_t)F + fc;
-      bulk.count = F - fc;
+      bulk.base = c.m * (int64_t)F + s.fc;
+      bulk.count = F - s.fc;
       bulk.alt = 0;
 #pragma unroll
       for (int i = 0; i < 8; ++i) bulk.v[i] = row[i];
-      fc = -1;
-      if (STATS) ++forwarded;
+      s.fc = -1;
+      if (STATS) ++s.forwarded;
       break;
     }
   }
+  return true;
+}
 
-  out.counts[m] = fc;
+// The end of a market's call: remaining fill rows, fill count, masks, ring
+// position, and the best bid/offer of the book as left (what get_bbo_kernel,
+// market.cu:280-320, would read) into the workspace's BBO cache. STATS also
+// adds the call's work counts.
+template <int W, bool STATS>
+ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx &c,
+                             const LoopState<W> &s, FillSink &sink) {
+  const int64_t M = b.M, m = c.m;
+  const int32_t L = c.L, O = c.O;
+  sink.flush(out, c.pf, c.C);
+  out.counts[m] = s.fc;
 #pragma unroll
   for (int i = 0; i < W; ++i) {
-    b.masks[(int64_t)i * M + m] = bm[i];
-    b.masks[(int64_t)(W + i) * M + m] = am[i];
+    b.masks[(int64_t)i * M + m] = s.bm[i];
+    b.masks[(int64_t)(W + i) * M + m] = s.am[i];
   }
-  b.next_slot[m] = ns;
+  b.next_slot[m] = c.ns;
 
-  // ---- best bid / offer of the book as left (what get_bbo_kernel reads) ----
   int32_t obs = 0, oas = 0;
-  if (bb >= 0 && bh < (uint32_t)O) {
-    if (have_b) obs = (int32_t)brec.x;
-    else if (fc == 0 && bh == aslot) obs = (int32_t)kra.x;
-    else if (fc == 0 && bh == bslot) obs = (int32_t)krb.x;
-    else obs = reinterpret_cast<const int32_t *>(rec + bh)[0];
+  if (s.bb >= 0 && s.bh < (uint32_t)O) {
+    if (s.have_b) obs = (int32_t)s.brec.x;
+    else if (s.fc == 0 && s.bh == c.aslot) obs = (int32_t)c.kra.x;
+    else if (s.fc == 0 && s.bh == c.bslot) obs = (int32_t)c.krb.x;
+    else obs = reinterpret_cast<const int32_t *>(c.rec + s.bh)[0];
   }
-  if (ba < L && ah < (uint32_t)O) {
-    if (have_a) oas = (int32_t)arec.x;
-    else if (fc == 0 && ah == aslot) oas = (int32_t)kra.x;
-    else if (fc == 0 && ah == bslot) oas = (int32_t)krb.x;
-    else oas = reinterpret_cast<const int32_t *>(rec + ah)[0];
+  if (s.ba < L && s.ah < (uint32_t)O) {
+    if (s.have_a) oas = (int32_t)s.arec.x;
+    else if (s.fc == 0 && s.ah == c.aslot) oas = (int32_t)c.kra.x;
+    else if (s.fc == 0 && s.ah == c.bslot) oas = (int32_t)c.krb.x;
+    else oas = reinterpret_cast<const int32_t *>(c.rec + s.ah)[0];
   }
-  b.bbo[m] = (bb >= 0 && bh < (uint32_t)O) ? bb : ASTRA_NULL_INDEX;
+  b.bbo[m] = (s.bb >= 0 && s.bh < (uint32_t)O) ? s.bb : ASTRA_NULL_INDEX;
   b.bbo[M + m] = obs;
-  b.bbo[2 * M + m] = (ba < L && ah < (uint32_t)O) ? ba : ASTRA_NULL_INDEX;
+  b.bbo[2 * M + m] = (s.ba < L && s.ah < (uint32_t)O) ? s.ba : ASTRA_NULL_INDEX;
   b.bbo[3 * M + m] = oas;
 
   if (STATS) {  // uniform addresses: the compiler aggregates these per wave
-    add_u64(b.stats + 0, (unsigned long long)(bid_ok + ask_ok));
-    add_u64(b.stats + 1, (unsigned long long)(fc < 0 ? F : fc));
-    add_u64(b.stats + 2, (unsigned long long)emptied);
-    add_u64(b.stats + 3, (unsigned long long)(fc < 0));
-    add_u64(b.stats + 4, (unsigned long long)forwarded);
+    add_u64(b.stats + 0, (unsigned long long)(c.bid_ok + c.ask_ok));
+    add_u64(b.stats + 1, (unsigned long long)(s.fc < 0 ? c.F : s.fc));
+    add_u64(b.stats + 2, (unsigned long long)s.emptied);
+    add_u64(b.stats + 3, (unsigned long long)(s.fc < 0));
+    add_u64(b.stats + 4, (unsigned long long)s.forwarded);
   }
 }
 
@@ -706,12 +885,83 @@ __device__ __forceinline__ void write_bulk_wave(const FillOut &out, const Bulk &
 }
 
 // All 64 lanes of a wavefront reach write_bulk_wave (no early return).
+// LDS per wavefront: the fill-row buffer during the first pass, then (when
+// staging is enabled for the shape) the staged book of one market.
+constexpr size_t kSinkBytesPerWave = 8 * kRows * 64 * sizeof(int32_t);
+constexpr size_t kMaxStageBytes = 32 * 1024;
+
+inline size_t stage_bytes(int32_t L, int32_t O) { return (size_t)O * 16 + (size_t)L * 8; }
+
+ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const int32_t lo = __shfl((int32_t)(uint32_t)v, src);
+  const int32_t hi = __shfl((int32_t)((uint64_t)v >> 32), src);
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+#else
+  (void)src;
+  return v;
+#endif
+}
+
+// Fused add + match + BBO, one lane per market, in two passes.
+//   1. Every lane runs its market's loop for at most `budget` passes.
+//   2. Markets still crossing after that (long walks through stale or
+//      consumed orders) are finished one at a time: the whole wavefront copies
+//      the market's order records and level words into LDS with coalesced
+//      loads, and the owning lane resumes its loop reading from LDS.
+// All 64 lanes of a wavefront reach the ballots (no early return).
 template <int W, bool STATS>
-__global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, FillOut out) {
+__global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, FillOut out,
+                                                          int32_t budget, int32_t wave_words) {
+  extern __shared__ int32_t lds_words[];
   const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = (int)(threadIdx.x % 64);
+  int32_t *wave_lds = lds_words + (threadIdx.x / 64) * wave_words;
   Bulk bulk;
   bulk.count = 0;
-  if (m < b.M) quote_match_market<W, STATS>(b, in, out, m, bulk);
+  FillSink sink;
+#if defined(__HIP_DEVICE_COMPILE__)
+  sink.lds = wave_lds;
+  sink.lane = lane;
+#endif
+  MarketCtx c;
+  LoopState<W> st;
+  bool suspended = false;
+  if (m < b.M) {
+    quote_prologue<W>(b, in, m, c, st);
+    sink.base = m * (int64_t)b.F;
+    const GlobalBook gb{c.lv, c.rec};
+    if (match_loop<W, STATS>(st, c, gb, sink, out, bulk, budget)) {
+      quote_epilogue<W, STATS>(b, out, c, st, sink);
+    } else {
+      sink.flush(out, c.pf, c.C);  // frees the LDS for staging
+      suspended = true;
+    }
+  }
+  uint64_t todo = __ballot(suspended);
+  while (todo) {
+    const int src = __ffsll((unsigned long long)todo) - 1;
+    todo &= todo - 1;
+    const int64_t ms = shfl_i64(m, src);
+    uint4 *srec = reinterpret_cast<uint4 *>(wave_lds);
+    uint64_t *slv = reinterpret_cast<uint64_t *>(srec + b.O);
+    const uint4 *grec = b.records + ms * (int64_t)b.O;
+    const uint64_t *glv = reinterpret_cast<const uint64_t *>(b.levels) + ms * (int64_t)b.L;
+    __builtin_amdgcn_wave_barrier();
+    for (int32_t i = lane; i < b.O; i += 64) srec[i] = grec[i];
+    for (int32_t i = lane; i < b.L; i += 64) slv[i] = glv[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == src) {
+      sink.direct = true;
+      const StagedBook sb{c.lv, c.rec, reinterpret_cast<uint16_t *>(slv), srec};
+      match_loop<W, STATS>(st, c, sb, sink, out, bulk, 0x7FFFFFFF);
+      quote_epilogue<W, STATS>(b, out, c, st, sink);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
   write_bulk_wave(out, bulk);
 }
 
@@ -757,24 +1007,47 @@ template <int W>
 int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &fo,
                        hipStream_t s) {
   const Book b = book_of(h);
+  const bool staged = h->stage_budget > 0 && stage_bytes(h->L, h->O) <= kMaxStageBytes;
+  const int32_t budget = staged ? h->stage_budget : 0x7FFFFFFF;
 #ifdef ASTRA_HOST_EMULATION
   (void)s;
+  std::vector<uint4> srec(staged ? (size_t)h->O : 0);
+  std::vector<uint16_t> slv(staged ? (size_t)h->L * 4 : 0);
   for (int64_t m = 0; m < b.M; ++m) {
     Bulk bulk;
     bulk.count = 0;
-    if (b.stats)
-      quote_match_market<W, true>(b, in, fo, m, bulk);
-    else
-      quote_match_market<W, false>(b, in, fo, m, bulk);
+    FillSink sink;
+    MarketCtx c;
+    LoopState<W> st;
+    quote_prologue<W>(b, in, m, c, st);
+    sink.base = m * (int64_t)b.F;
+    const GlobalBook gb{c.lv, c.rec};
+    const bool done = b.stats ? match_loop<W, true>(st, c, gb, sink, fo, bulk, budget)
+                              : match_loop<W, false>(st, c, gb, sink, fo, bulk, budget);
+    if (!done) {  // the second pass, as on the GPU
+      sink.flush(fo, c.pf, c.C);
+      std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
+      std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
+      sink.direct = true;
+      const StagedBook sb{c.lv, c.rec, slv.data(), srec.data()};
+      if (b.stats) match_loop<W, true>(st, c, sb, sink, fo, bulk, 0x7FFFFFFF);
+      else match_loop<W, false>(st, c, sb, sink, fo, bulk, 0x7FFFFFFF);
+    }
+    if (b.stats) quote_epilogue<W, true>(b, fo, c, st, sink);
+    else quote_epilogue<W, false>(b, fo, c, st, sink);
     if (bulk.count > 0) write_bulk_host(fo, bulk);
   }
 #else
+  const size_t wave_bytes =
+      std::max(kSinkBytesPerWave, staged ? align_up(stage_bytes(h->L, h->O), 16) : (size_t)0);
+  const size_t lds = (size_t)(h->block / 64) * wave_bytes;
+  const int32_t wave_words = (int32_t)(wave_bytes / 4);
   if (b.stats)
     hipLaunchKernelGGL((quote_match_kernel<W, true>), dim3(grid_for(b.M, h->block)),
-                       dim3(h->block), 0, s, b, in, fo);
+                       dim3(h->block), lds, s, b, in, fo, budget, wave_words);
   else
     hipLaunchKernelGGL((quote_match_kernel<W, false>), dim3(grid_for(b.M, h->block)),
-                       dim3(h->block), 0, s, b, in, fo);
+                       dim3(h->block), lds, s, b, in, fo, budget, wave_words);
 #endif
   ASTRA_HIP_CHECK(rt_last_error(), "AddTwoSidedQuotes");
   return ASTRA_OK;
@@ -888,6 +1161,15 @@ int validate_shape(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, int32_
   return ASTRA_OK;
 }
 
+int default_stage_budget() {
+  const char *e = std::getenv("ASTRA_MARKET_STAGE_BUDGET");
+  if (e) {
+    const int v = std::atoi(e);
+    if (v >= 0) return v;
+  }
+  return 16;
+}
+
 int default_block() {
   const char *e = std::getenv("ASTRA_MARKET_BLOCK");
   if (e) {
@@ -960,6 +1242,7 @@ int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, i
   h->flags = flags;
   h->tid = 0;
   h->block = default_block();
+  h->stage_budget = default_stage_budget();
   h->stats = nullptr;
   h->ws = static_cast<char *>(workspace);
   h->ws_bytes = workspace_bytes;

@@ -53,6 +53,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the all-thread oracle leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--phases", default="ABCD",
+                    help="phases to run (A is always run; B latency, C events, D work counts)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for rocprof counter scaling)")
     return ap.parse_args()
@@ -132,7 +134,9 @@ def main():
     for t in range(W):
         step(market, t)
     torch.cuda.synchronize()
-    snaps = [market.clone() for _ in range(3)]  # state at the start of the timed steps
+    phases = set(args.phases.upper()) | {"A"}
+    # state at the start of the timed steps, for the replays B, C and D
+    snaps = [market.clone() if p in phases else None for p in "BCD"]
     torch.cuda.synchronize()
     log(f"warm-up done ({W} steps); timing {K} steps")
 
@@ -146,8 +150,10 @@ def main():
     log(f"A: {K} steps in {wall * 1e3:.2f} ms")
 
     # ---- B: per-step latency (stream synced every step) ----
-    nlat = min(K, args.latency_steps)
-    lat = []
+    nlat = min(K, args.latency_steps) if "B" in phases else 0
+    lat = [float("nan")]
+    if nlat:
+        lat = []
     for t in range(W, W + nlat):
         torch.cuda.synchronize()
         h0 = time.perf_counter()
@@ -157,9 +163,10 @@ def main():
     lat_ms = np.array(lat) * 1e3
 
     # ---- C: device time per kernel (HIP events on the launch stream) ----
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    nev = K if "C" in phases else 0
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(nev)]
     torch.cuda.synchronize()
-    for i, t in enumerate(range(W, T)):
+    for i, t in enumerate(range(W, W + nev)):
         e = evs[i]
         e[0].record()
         snaps[1].add_two_sided_quotes(*rows[t], fills)
@@ -168,17 +175,18 @@ def main():
             snaps[1].get_bbos(bbos)
         e[2].record()
     torch.cuda.synchronize()
-    qm_ms = np.array([e[0].elapsed_time(e[1]) for e in evs])
-    bbo_ms = np.array([e[1].elapsed_time(e[2]) for e in evs]) if bbo else np.zeros(K)
+    qm_ms = np.array([e[0].elapsed_time(e[1]) for e in evs]) if nev else np.array([wall / K * 1e3])
+    bbo_ms = np.array([e[1].elapsed_time(e[2]) for e in evs]) if (bbo and nev) else np.zeros(1)
 
     # ---- D: exact work counts for the algorithmic bytes ----
     counters = torch.zeros(8, dtype=torch.int64, device=dev)
-    snaps[2]._set_stats(counters)
-    for t in range(W, T):
-        snaps[2].add_two_sided_quotes(*rows[t], fills)
-    torch.cuda.synchronize()
+    if "D" in phases:
+        snaps[2]._set_stats(counters)
+        for t in range(W, T):
+            snaps[2].add_two_sided_quotes(*rows[t], fills)
+        torch.cuda.synchronize()
+        snaps[2]._set_stats(None)
     n_ins, n_fill, n_empty, n_ovf, n_ff = (int(x) for x in counters.cpu().tolist()[:5])
-    snaps[2]._set_stats(None)
     log(f"work over {K} steps: inserts {n_ins}, fill rows {n_fill}, emptied {n_empty}, overflow {n_ovf}")
 
     # algorithmic bytes (per launch of the matching kernel): quotes in 20 B + fill_counts 4 B

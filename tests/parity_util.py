@@ -106,18 +106,36 @@ def compare_portfolios(gpu_mk, ora_mk, where: str):
         raise AssertionError(f"{where}: portfolios differ at {bad.tolist()}")
 
 
+def make_market(M, L, O, F, C, extended=None, stage_budget=None):
+    """VecMarket through the drop-in API. stage_budget (read by the engine when the
+    market is created) sets the loop passes before a market's book is staged in
+    LDS; 1 forces the staged path for every market that crosses twice."""
+    import os
+    from astra_cuda import order_matching as aom
+    if extended is None:
+        extended = L > 128 or O > 1024 or F > 1024 or C > 1024
+    old = os.environ.get("ASTRA_MARKET_STAGE_BUDGET")
+    if stage_budget is not None:
+        os.environ["ASTRA_MARKET_STAGE_BUDGET"] = str(stage_budget)
+    try:
+        return aom.VecMarket(M, L, O, F, C, allow_extended_shapes=extended)
+    finally:
+        if stage_budget is not None:
+            if old is None:
+                del os.environ["ASTRA_MARKET_STAGE_BUDGET"]
+            else:
+                os.environ["ASTRA_MARKET_STAGE_BUDGET"] = old
+
+
 def run_parity(M, L, O, F, C, steps, gen, *, bbo_every=1, full_every=0, last_every=1,
-               extended=None, nthreads=8, label=""):
+               extended=None, nthreads=8, label="", stage_budget=None):
     """Drive GPU engine and oracle with the same inputs; compare after every step.
 
     ``gen(t)`` returns (bid_px, bid_sz, ask_px, ask_sz, cust) int32 arrays of shape [M].
     Returns summary statistics (fill rows compared, overflows seen).
     """
-    from astra_cuda import order_matching as aom
     from oracle.oracle import OracleMarket
-    if extended is None:
-        extended = L > 128 or O > 1024 or F > 1024 or C > 1024
-    g = aom.VecMarket(M, L, O, F, C, allow_extended_shapes=extended)
+    g = make_market(M, L, O, F, C, extended, stage_budget)
     gf, gb = g.new_fill_batch(), g.new_bbo_batch()
     o = OracleMarket(M, L, O, F, C)
     of, ob = o.new_fill_batch(), o.new_bbo_batch()

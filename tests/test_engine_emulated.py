@@ -6,6 +6,8 @@ mask/level/record bookkeeping under eviction aliasing, and the diagnostic work
 counters. The GPU parity tests (test_gpu_*.py) repeat the parity checks on the
 device build.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -34,8 +36,24 @@ def _compare(em, ef, eb, om, of, ob, F, where):
     assert np.array_equal(em.portfolios, om.customer_portfolios), where
 
 
-def _run(M, L, O, F, C, steps, gen, with_stats=False):
-    em, om = EmuMarket(M, L, O, F, C), OracleMarket(M, L, O, F, C)
+def _emu(M, L, O, F, C, stage_budget=None):
+    """Emulated engine; stage_budget sets the passes before a market's book is staged
+    (0: never), read by the engine when the market is created."""
+    if stage_budget is None:
+        return EmuMarket(M, L, O, F, C)
+    old = os.environ.get("ASTRA_MARKET_STAGE_BUDGET")
+    os.environ["ASTRA_MARKET_STAGE_BUDGET"] = str(stage_budget)
+    try:
+        return EmuMarket(M, L, O, F, C)
+    finally:
+        if old is None:
+            del os.environ["ASTRA_MARKET_STAGE_BUDGET"]
+        else:
+            os.environ["ASTRA_MARKET_STAGE_BUDGET"] = old
+
+
+def _run(M, L, O, F, C, steps, gen, with_stats=False, stage_budget=None):
+    em, om = _emu(M, L, O, F, C, stage_budget), OracleMarket(M, L, O, F, C)
     ef, of = em.new_fill_batch(), om.new_fill_batch()
     eb, ob = em.new_bbo_batch(), om.new_bbo_batch()
     stats = np.zeros(8, np.int64)
@@ -74,8 +92,9 @@ ALIAS_CASES = [
 ]
 
 
+@pytest.mark.parametrize("stage_budget", [None, 0, 1, 3])
 @pytest.mark.parametrize("M,L,O,F,C,steps,seed", ALIAS_CASES)
-def test_emulated_aliasing_vs_oracle(M, L, O, F, C, steps, seed):
+def test_emulated_aliasing_vs_oracle(M, L, O, F, C, steps, seed, stage_budget):
     rng = np.random.default_rng(seed)
     hot = max(4, min(L, 24))
 
@@ -88,7 +107,7 @@ def test_emulated_aliasing_vs_oracle(M, L, O, F, C, steps, seed):
         return (bid, rng.integers(-1, 8, M).astype(np.int32), ask,
                 rng.integers(-1, 8, M).astype(np.int32), rng.integers(-1, C + 2, M).astype(np.int32))
 
-    _, _, st = _run(M, L, O, F, C, steps, gen, with_stats=True)
+    _, _, st = _run(M, L, O, F, C, steps, gen, with_stats=True, stage_budget=stage_budget)
     # tiny rings exercise both overflow routes: the repeating-state fast-forward
     # and the ordinary F-th fill (with O = 1 every overflow repeats)
     assert st["fast_forwards"] > 0
@@ -104,12 +123,13 @@ def test_emulated_config1_full_run():
     assert st["fills"] > 0
 
 
-def test_emulated_config3_and_4_samples():
+@pytest.mark.parametrize("stage_budget", [None, 1])
+def test_emulated_config3_and_4_samples(stage_budget):
     from astra_cuda.workloads import CONFIGS, QuoteStream
     for idx, M, steps in ((3, 300, 700), (4, 60, 400)):
         cfg = CONFIGS[idx]
         qs = QuoteStream(cfg, np.arange(M))
-        _run(M, cfg.L, cfg.O, cfg.F, cfg.C, steps, qs.step, with_stats=True)
+        _run(M, cfg.L, cfg.O, cfg.F, cfg.C, steps, qs.step, with_stats=True, stage_budget=stage_budget)
 
 
 def test_emulated_reset_clear_clone_to_string():

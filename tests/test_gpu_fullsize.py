@@ -1,7 +1,7 @@
 """Config 3 at full size (100,000 markets x 1000 steps) against the oracle (GPU).
 
-Per step, the fill rows each call wrote, fill_counts and the four BBO arrays are
-reduced to weighted sums (a checksum per step; the list of them is the run's
+Per step, the fill rows each call wrote (gathered by (market, row) index),
+fill_counts and the four BBO arrays are reduced to weighted sums (a checksum per step; the list of them is the run's
 checksum of checksums) on each side, the GPU side in torch on the device, the
 oracle side in numpy. Weights are < 2^20 and all values here are small, so the
 int64 sums never overflow and both sides compute the same exact integers; a
@@ -24,33 +24,34 @@ BBO = ("best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes")
 _P = (1 << 20) - 3
 
 
-def _weights(M, kmax, salt, xp):
+def _rows(eff, xp):
+    """(market, k) of every fill row the last call wrote: k < eff[market]."""
     if xp is torch:
-        m = torch.arange(M, dtype=torch.int64, device=DEV)[:, None]
-        k = torch.arange(kmax, dtype=torch.int64, device=DEV)[None, :]
+        m = torch.repeat_interleave(torch.arange(eff.shape[0], device=DEV), eff.to(torch.int64))
+        start = torch.cumsum(eff.to(torch.int64), 0) - eff.to(torch.int64)
+        k = torch.arange(m.shape[0], device=DEV) - torch.repeat_interleave(start, eff.to(torch.int64))
     else:
-        m = np.arange(M, dtype=np.int64)[:, None]
-        k = np.arange(kmax, dtype=np.int64)[None, :]
-    return (m * 2654435761 + k * 40503 + salt * 97) % _P + 1
+        m = np.repeat(np.arange(eff.shape[0]), eff)
+        start = np.cumsum(eff) - eff
+        k = np.arange(m.shape[0]) - np.repeat(start, eff)
+    return m, k
 
 
-def _fill_digest(arrays, eff, kmax, xp):
-    M = eff.shape[0]
-    if kmax == 0:
-        return [0] * len(FIELDS)
-    valid = (xp.arange(kmax, device=DEV)[None, :] if xp is torch else np.arange(kmax)[None, :]) < eff[:, None]
+def _fill_digest(arrays, eff, xp):
+    m, k = _rows(eff, xp)
+    w0 = (m * 2654435761 + k * 40503) % _P + 1
     out = []
     for i, a in enumerate(arrays):
-        a = a[:, :kmax]
-        a = a.to(torch.int64) if xp is torch else a.astype(np.int64)
-        w = _weights(M, kmax, i, xp)
-        out.append(int((a * w * valid).sum()))
+        v = a[m, k]
+        v = v.to(torch.int64) if xp is torch else v.astype(np.int64)
+        out.append(int((v * ((w0 + i * 97) % _P + 1)).sum()))
     return out
 
 
 def _vec_digest(v, salt, xp):
     M = v.shape[0]
-    w = _weights(M, 1, salt + 50, xp)[:, 0]
+    m = torch.arange(M, dtype=torch.int64, device=DEV) if xp is torch else np.arange(M, dtype=np.int64)
+    w = (m * 2654435761 + (salt + 50) * 97) % _P + 1
     v = v.to(torch.int64) if xp is torch else v.astype(np.int64)
     return int((v * w).sum())
 
@@ -81,10 +82,9 @@ def test_gpu_config3_full_size_checksums():
         gc = gf.fill_counts
         assert _vec_digest(gc, 0, torch) == _vec_digest(oc, 0, np), f"step {t}: fill_counts"
         eff_o = effective_counts(oc, F)
-        kmax = int(eff_o.max())
         eff_g = torch.where(gc < 0, torch.full_like(gc, F), gc)
-        dg = _fill_digest([getattr(gf, f) for f in FIELDS], eff_g, kmax, torch)
-        do = _fill_digest([getattr(of, f) for f in FIELDS], eff_o, kmax, np)
+        dg = _fill_digest([getattr(gf, f) for f in FIELDS], eff_g, torch)
+        do = _fill_digest([getattr(of, f) for f in FIELDS], eff_o, np)
         assert dg == do, f"step {t}: fill digests differ {dg} vs {do}"
         for i, f in enumerate(BBO):
             assert _vec_digest(getattr(gb, f), i + 1, torch) == _vec_digest(getattr(ob, f), i + 1, np), \
@@ -96,4 +96,4 @@ def test_gpu_config3_full_size_checksums():
                 f"step {t}: portfolios"
             print(f"  step {t}: ok, {total_rows} fill rows so far, {time.time() - t0:.1f}s", flush=True)
     assert total_rows > cfg.M  # the workload trades
-    assert overflow == 0
+    assert overflow > 0  # ring reuse drives some books into the overflow state

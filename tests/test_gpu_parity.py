@@ -56,12 +56,15 @@ def test_gpu_config2_subset():
     assert r["fill_rows"] > 3000
 
 
-def test_gpu_config3_subset_with_eviction():
-    """Config 3 markets 0..3999 for all 1000 steps (the ring of 1024 wraps after 512 steps)."""
+@pytest.mark.parametrize("stage_budget", [None, 1])
+def test_gpu_config3_subset_with_eviction(stage_budget):
+    """Config 3 markets 0..3999 for all 1000 steps (the ring of 1024 wraps after 512 steps).
+    With stage_budget=1 every market that crosses twice in a call finishes on the
+    LDS-staged path."""
     cfg, gen = _stream_gen(3, np.arange(4000))
-    _log("config 3 subset: 4000 x 1000")
+    _log(f"config 3 subset: 4000 x 1000, stage budget {stage_budget}")
     r = run_parity(4000, cfg.L, cfg.O, cfg.F, cfg.C, 1000, gen, bbo_every=1, full_every=250,
-                   label="cfg3")
+                   label="cfg3", stage_budget=stage_budget)
     assert r["fill_rows"] > 4000
 
 
@@ -89,9 +92,10 @@ ALIAS_CASES = [
 ]
 
 
+@pytest.mark.parametrize("stage_budget", [None, 1])
 @pytest.mark.parametrize("M,L,O,F,C,steps,seed", ALIAS_CASES)
-def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed):
-    _log(f"aliasing M={M} L={L} O={O} F={F}")
+def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget):
+    _log(f"aliasing M={M} L={L} O={O} F={F} stage budget {stage_budget}")
     rng = np.random.default_rng(seed)
     hot = max(4, min(L, 24))  # concentrate prices so books cross often
 
@@ -104,7 +108,8 @@ def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed):
         return (bid, rng.integers(-1, 8, M).astype(np.int32), ask,
                 rng.integers(-1, 8, M).astype(np.int32), rng.integers(-1, C + 2, M).astype(np.int32))
 
-    r = run_parity(M, L, O, F, C, steps, gen, full_every=50, label=f"alias L{L} O{O}")
+    r = run_parity(M, L, O, F, C, steps, gen, full_every=50, label=f"alias L{L} O{O}",
+                   stage_budget=stage_budget)
     if O <= 3:
         assert r["overflows"] > 0
 
