@@ -1007,7 +1007,10 @@ template <int W>
 int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &fo,
                        hipStream_t s) {
   const Book b = book_of(h);
-  const bool staged = h->stage_budget > 0 && stage_bytes(h->L, h->O) <= kMaxStageBytes;
+  // Staging needs the market's records and level words in LDS next to the
+  // block's other wavefronts' buffers, within 64 KB per workgroup.
+  const bool staged = h->stage_budget > 0 && stage_bytes(h->L, h->O) <= kMaxStageBytes &&
+                      (size_t)(h->block / 64) * align_up(stage_bytes(h->L, h->O), 16) <= 65536;
   const int32_t budget = staged ? h->stage_budget : 0x7FFFFFFF;
 #ifdef ASTRA_HOST_EMULATION
   (void)s;
