@@ -346,11 +346,12 @@ inline void write_bulk_host(const FillOut &out, const Bulk &bk) {
 
 // Portfolio update of one fill row (market.cu:221-232): the buyer is the bid
 // side's customer, i.e. the taker when the ask quotes and the quoter otherwise.
-// A self-trade nets to zero, so it is skipped.
+// A self-trade or a zero quantity changes nothing, so it is skipped.
 ASTRA_HD void apply_portfolio(int32_t *pf, int32_t C, int32_t price, int32_t qty, int32_t taker,
                               int32_t quoter, bool ask_quotes) {
   const int32_t buyer = ask_quotes ? taker : quoter, seller = ask_quotes ? quoter : taker;
-  if ((uint32_t)buyer < (uint32_t)C && (uint32_t)seller < (uint32_t)C && buyer != seller) {
+  if (qty != 0 && (uint32_t)buyer < (uint32_t)C && (uint32_t)seller < (uint32_t)C &&
+      buyer != seller) {
     const uint32_t notional = (uint32_t)price * (uint32_t)qty;
     add_i32(pf + 2 * buyer, qty);
     add_i32(pf + 2 * buyer + 1, (int32_t)(0u - notional));
@@ -364,23 +365,24 @@ ASTRA_HD void apply_portfolio(int32_t *pf, int32_t C, int32_t price, int32_t qty
 // words: no bank conflicts); the host build keeps them in a local array. Rows
 // go out kRows at a time as aligned vector stores (rows k..k+kRows-1 of one
 // market are contiguous in each field array), together with the portfolio
-// updates they imply. In direct mode (used once the LDS holds a staged book)
-// each row is written as it comes. Nothing beyond the call's last row is ever
-// written: the reference leaves later entries of a FillBatch untouched.
+// updates they imply. Once the LDS holds a staged book, the one lane still
+// working uses a small buffer after it (stride 1). Nothing beyond the call's
+// last row is ever written: the reference leaves later entries of a FillBatch
+// untouched.
 constexpr int kRows = 4;
 
 struct FillSink {
 #if defined(__HIP_DEVICE_COMPILE__)
-  int32_t *lds;  // this wavefront's [8][kRows][64] buffer
+  int32_t *lds;  // [8][kRows][stride] buffer: stride 64 (one column per lane) or 1
   int lane;
-  __device__ int32_t &at(int f, int r) const { return lds[(f * kRows + r) * 64 + lane]; }
+  int stride;
+  __device__ int32_t &at(int f, int r) const { return lds[(f * kRows + r) * stride + lane]; }
 #else
   mutable int32_t buf[8][kRows];
   int32_t &at(int f, int r) const { return buf[f][r]; }
 #endif
   int64_t base = 0;  // fill index of buffered row 0
   int32_t n = 0;     // rows buffered
-  bool direct = false;
 
   ASTRA_HD void flush(const FillOut &out, int32_t *pf, int32_t C) {
     if (n == 0) return;
@@ -423,11 +425,6 @@ struct FillSink {
   }
 
   ASTRA_HD void put(const FillOut &out, int32_t *pf, int32_t C, const int32_t (&row)[8]) {
-    if (direct) {
-      write_fill(out, base++, row);
-      apply_portfolio(pf, C, row[0], row[1], row[2], row[3], row[4] != 0);
-      return;
-    }
 #pragma unroll
     for (int f = 0; f < 8; ++f) at(f, n) = row[f];
     if (++n == kRows) flush(out, pf, C);
@@ -889,8 +886,13 @@ __device__ __forceinline__ void write_bulk_wave(const FillOut &out, const Bulk &
 // staging is enabled for the shape) the staged book of one market.
 constexpr size_t kSinkBytesPerWave = 8 * kRows * 64 * sizeof(int32_t);
 constexpr size_t kMaxStageBytes = 32 * 1024;
+typedef __attribute__((address_space(1))) void gvoid_t;  // global memory
+typedef __attribute__((address_space(3))) void lvoid_t;  // LDS
 
-inline size_t stage_bytes(int32_t L, int32_t O) { return (size_t)O * 16 + (size_t)L * 8; }
+// Staged book of one market: records, level words, then a one-lane row buffer.
+inline size_t stage_bytes(int32_t L, int32_t O) {
+  return (size_t)O * 16 + (size_t)L * 8 + 8 * kRows * sizeof(int32_t);
+}
 
 ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -923,6 +925,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
 #if defined(__HIP_DEVICE_COMPILE__)
   sink.lds = wave_lds;
   sink.lane = lane;
+  sink.stride = 64;
 #endif
   MarketCtx c;
   LoopState<W> st;
@@ -948,13 +951,31 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     const uint4 *grec = b.records + ms * (int64_t)b.O;
     const uint64_t *glv = reinterpret_cast<const uint64_t *>(b.levels) + ms * (int64_t)b.L;
     __builtin_amdgcn_wave_barrier();
-    for (int32_t i = lane; i < b.O; i += 64) srec[i] = grec[i];
-    for (int32_t i = lane; i < b.L; i += 64) slv[i] = glv[i];
+#if defined(__HIP_DEVICE_COMPILE__)
+    // LDS DMA (global_load_lds): each lane's 16 (or 4) bytes go straight to
+    // LDS at the wave-uniform base + lane * size, no registers involved, all
+    // loads in flight together.
+    for (int32_t j = 0; j < b.O; j += 64)
+      if (j + lane < b.O)
+        __builtin_amdgcn_global_load_lds((gvoid_t *)(grec + j + lane), (lvoid_t *)(srec + j), 16, 0,
+                                         0);
+    const uint32_t *glv32 = reinterpret_cast<const uint32_t *>(glv);
+    uint32_t *slv32 = reinterpret_cast<uint32_t *>(slv);
+    for (int32_t j = 0; j < 2 * b.L; j += 64)
+      if (j + lane < 2 * b.L)
+        __builtin_amdgcn_global_load_lds((gvoid_t *)(glv32 + j + lane), (lvoid_t *)(slv32 + j), 4,
+                                         0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+#endif
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (lane == src) {
-      sink.direct = true;
+#if defined(__HIP_DEVICE_COMPILE__)
+      sink.lds = reinterpret_cast<int32_t *>(slv + b.L);
+      sink.lane = 0;
+      sink.stride = 1;
+#endif
       const StagedBook sb{c.lv, c.rec, reinterpret_cast<uint16_t *>(slv), srec};
       match_loop<W, STATS>(st, c, sb, sink, out, bulk, 0x7FFFFFFF);
       quote_epilogue<W, STATS>(b, out, c, st, sink);
@@ -1031,7 +1052,6 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
       sink.flush(fo, c.pf, c.C);
       std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
       std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
-      sink.direct = true;
       const StagedBook sb{c.lv, c.rec, slv.data(), srec.data()};
       if (b.stats) match_loop<W, true>(st, c, sb, sink, fo, bulk, 0x7FFFFFFF);
       else match_loop<W, false>(st, c, sb, sink, fo, bulk, 0x7FFFFFFF);
