@@ -365,18 +365,15 @@ ASTRA_HD void apply_portfolio(int32_t *pf, int32_t C, int32_t price, int32_t qty
 // words: no bank conflicts); the host build keeps them in a local array. Rows
 // go out kRows at a time as aligned vector stores (rows k..k+kRows-1 of one
 // market are contiguous in each field array), together with the portfolio
-// updates they imply. Once the LDS holds a staged book, the one lane still
-// working uses a small buffer after it (stride 1). Nothing beyond the call's
-// last row is ever written: the reference leaves later entries of a FillBatch
-// untouched.
+// updates they imply. Nothing beyond the call's last row is ever written: the
+// reference leaves later entries of a FillBatch untouched.
 constexpr int kRows = 4;
 
 struct FillSink {
 #if defined(__HIP_DEVICE_COMPILE__)
-  int32_t *lds;  // [8][kRows][stride] buffer: stride 64 (one column per lane) or 1
+  int32_t *lds;  // this wavefront's [8][kRows][64] buffer
   int lane;
-  int stride;
-  __device__ int32_t &at(int f, int r) const { return lds[(f * kRows + r) * stride + lane]; }
+  __device__ int32_t &at(int f, int r) const { return lds[(f * kRows + r) * 64 + lane]; }
 #else
   mutable int32_t buf[8][kRows];
   int32_t &at(int f, int r) const { return buf[f][r]; }
@@ -424,12 +421,45 @@ struct FillSink {
     n = 0;
   }
 
+  ASTRA_HD bool full() const { return false; }  // flushes itself
+
   ASTRA_HD void put(const FillOut &out, int32_t *pf, int32_t C, const int32_t (&row)[8]) {
 #pragma unroll
     for (int f = 0; f < 8; ++f) at(f, n) = row[f];
     if (++n == kRows) flush(out, pf, C);
   }
 };
+
+// Rows of the one market being finished on a staged book: [cap][8] words (LDS
+// on the GPU). When it is full the loop stops and the whole wavefront writes
+// the rows out (flush_rows), coalesced, then the loop resumes.
+constexpr int32_t kStageRows = 64;
+
+struct RowBuffer {
+  int32_t *rows;
+  int32_t cap;
+  int32_t n;
+  int64_t base;  // fill index of row 0
+  ASTRA_HD bool full() const { return n == cap; }
+  ASTRA_HD void put(const FillOut &, int32_t *, int32_t, const int32_t (&row)[8]) {
+#pragma unroll
+    for (int f = 0; f < 8; ++f) rows[n * 8 + f] = row[f];
+    ++n;
+  }
+};
+
+// Rows [first, n) of a row buffer, `step` rows apart (64 lanes: row r by lane
+// r % 64, so each field's stores are coalesced), with their portfolio updates.
+ASTRA_HD void flush_rows(const FillOut &out, const int32_t *rows, int32_t n, int64_t base,
+                         int32_t *pf, int32_t C, int32_t first, int32_t step) {
+  for (int32_t r = first; r < n; r += step) {
+    int32_t v[8];
+#pragma unroll
+    for (int f = 0; f < 8; ++f) v[f] = rows[r * 8 + f];
+    write_fill(out, base + r, v);
+    apply_portfolio(pf, C, v[0], v[1], v[2], v[3], v[4] != 0);
+  }
+}
 
 // What stays fixed for a market during its matching loop.
 struct MarketCtx {
@@ -460,13 +490,14 @@ struct LoopState {
 };
 
 // The book as the loop sees it. GlobalBook: the market's arrays in global
-// memory. StagedBook: reads from a copy of the market's records and level
-// words (in LDS on the GPU) and writes to both copies, so global memory stays
-// current.
+// memory. StagedBook: a copy of the market's records and level words (in LDS
+// on the GPU) that the loop reads and writes; it is copied back to global
+// memory when the market is done.
 struct GlobalBook {
   uint16_t *lv;
   uint4 *rec;
   ASTRA_HD uint4 record(uint32_t s) const { return rec[s]; }
+  ASTRA_HD int32_t size(uint32_t s) const { return reinterpret_cast<const int32_t *>(rec + s)[0]; }
   ASTRA_HD uint32_t word(int32_t p, int side) const { return level_word(lv, p, side); }
   ASTRA_HD void set_size(uint32_t s, int32_t v) const {
     reinterpret_cast<int32_t *>(rec + s)[0] = v;
@@ -476,24 +507,18 @@ struct GlobalBook {
 };
 
 struct StagedBook {
-  uint16_t *lv;
-  uint4 *rec;
   uint16_t *slv;
   uint4 *srec;
   ASTRA_HD uint4 record(uint32_t s) const { return srec[s]; }
+  ASTRA_HD int32_t size(uint32_t s) const { return reinterpret_cast<const int32_t *>(srec + s)[0]; }
   ASTRA_HD uint32_t word(int32_t p, int side) const { return level_word(slv, p, side); }
   ASTRA_HD void set_size(uint32_t s, int32_t v) const {
     reinterpret_cast<int32_t *>(srec + s)[0] = v;
-    reinterpret_cast<int32_t *>(rec + s)[0] = v;
   }
   ASTRA_HD void set_word(int32_t p, int side, uint32_t w) const {
     store_level_word(slv, p, side, w);
-    store_level_word(lv, p, side, w);
   }
-  ASTRA_HD void set_head(int32_t p, int side, uint32_t h) const {
-    store_head(slv, p, side, h);
-    store_head(lv, p, side, h);
-  }
+  ASTRA_HD void set_head(int32_t p, int side, uint32_t h) const { store_head(slv, p, side, h); }
 };
 
 // add_orders_kernel (market.cu:17-100) for market m and the set-up of the
@@ -614,8 +639,8 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
 }
 
 // match_orders_kernel's crossing loop (market.cu:145-274). Runs at most
-// `budget` passes; returns false (state intact, nothing of the next pass done)
-// when the budget ran out first.
+// `budget` passes and stops early when the sink is full; returns false (state
+// intact, nothing of the next pass done) when it stopped before the end.
 //
 // Two loop states repeat forever (both arise from ring-slot reuse): a size-0
 // head that links to itself (each pass emits the same zero-size fill and
@@ -623,14 +648,14 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
 // s and -s alternate). The reference loops until F fills and then writes -1;
 // here the owed rows are handed to the caller in `bulk`, the final state is set
 // directly, and the count is -1, which is the same result.
-template <int W, bool STATS, class BookMem>
-ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, FillSink &sink,
+template <int W, bool STATS, class BookMem, class Sink>
+ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, Sink &sink,
                          const FillOut &out, Bulk &bulk, int32_t budget) {
   const int32_t L = c.L, O = c.O, F = c.F;
   int32_t passes = 0;
   while (s.bb >= 0 && s.ba < L && s.bb >= s.ba) {
     if (s.bh >= (uint32_t)O || s.ah >= (uint32_t)O) break;  // NULL head (:155)
-    if (passes++ >= budget) return false;
+    if (passes++ >= budget || sink.full()) return false;
     // Records: before the first fill nothing has changed, so the inserted
     // records come from registers; after that every size change has been
     // written through, so memory is current.
@@ -764,9 +789,9 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
 // position, and the best bid/offer of the book as left (what get_bbo_kernel,
 // market.cu:280-320, would read) into the workspace's BBO cache. STATS also
 // adds the call's work counts.
-template <int W, bool STATS>
+template <int W, bool STATS, class BookMem>
 ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx &c,
-                             const LoopState<W> &s, FillSink &sink) {
+                             const LoopState<W> &s, FillSink &sink, const BookMem &bk) {
   const int64_t M = b.M, m = c.m;
   const int32_t L = c.L, O = c.O;
   sink.flush(out, c.pf, c.C);
@@ -783,13 +808,13 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
     if (s.have_b) obs = (int32_t)s.brec.x;
     else if (s.fc == 0 && s.bh == c.aslot) obs = (int32_t)c.kra.x;
     else if (s.fc == 0 && s.bh == c.bslot) obs = (int32_t)c.krb.x;
-    else obs = reinterpret_cast<const int32_t *>(c.rec + s.bh)[0];
+    else obs = bk.size(s.bh);
   }
   if (s.ba < L && s.ah < (uint32_t)O) {
     if (s.have_a) oas = (int32_t)s.arec.x;
     else if (s.fc == 0 && s.ah == c.aslot) oas = (int32_t)c.kra.x;
     else if (s.fc == 0 && s.ah == c.bslot) oas = (int32_t)c.krb.x;
-    else oas = reinterpret_cast<const int32_t *>(c.rec + s.ah)[0];
+    else oas = bk.size(s.ah);
   }
   b.bbo[m] = (s.bb >= 0 && s.bh < (uint32_t)O) ? s.bb : ASTRA_NULL_INDEX;
   b.bbo[M + m] = obs;
@@ -889,9 +914,9 @@ constexpr size_t kMaxStageBytes = 32 * 1024;
 typedef __attribute__((address_space(1))) void gvoid_t;  // global memory
 typedef __attribute__((address_space(3))) void lvoid_t;  // LDS
 
-// Staged book of one market: records, level words, then a one-lane row buffer.
+// Staged book of one market: records, level words, then its row buffer.
 inline size_t stage_bytes(int32_t L, int32_t O) {
-  return (size_t)O * 16 + (size_t)L * 8 + 8 * kRows * sizeof(int32_t);
+  return (size_t)O * 16 + (size_t)L * 8 + (size_t)kStageRows * 8 * sizeof(int32_t);
 }
 
 ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
@@ -925,7 +950,6 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
 #if defined(__HIP_DEVICE_COMPILE__)
   sink.lds = wave_lds;
   sink.lane = lane;
-  sink.stride = 64;
 #endif
   MarketCtx c;
   LoopState<W> st;
@@ -935,7 +959,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     sink.base = m * (int64_t)b.F;
     const GlobalBook gb{c.lv, c.rec};
     if (match_loop<W, STATS>(st, c, gb, sink, out, bulk, budget)) {
-      quote_epilogue<W, STATS>(b, out, c, st, sink);
+      quote_epilogue<W, STATS>(b, out, c, st, sink, gb);
     } else {
       sink.flush(out, c.pf, c.C);  // frees the LDS for staging
       suspended = true;
@@ -948,8 +972,10 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     const int64_t ms = shfl_i64(m, src);
     uint4 *srec = reinterpret_cast<uint4 *>(wave_lds);
     uint64_t *slv = reinterpret_cast<uint64_t *>(srec + b.O);
-    const uint4 *grec = b.records + ms * (int64_t)b.O;
-    const uint64_t *glv = reinterpret_cast<const uint64_t *>(b.levels) + ms * (int64_t)b.L;
+    int32_t *rows = reinterpret_cast<int32_t *>(slv + b.L);
+    uint4 *grec = b.records + ms * (int64_t)b.O;
+    uint64_t *glv = reinterpret_cast<uint64_t *>(b.levels) + ms * (int64_t)b.L;
+    int32_t *pfm = b.portfolios + ms * (int64_t)b.C * 2;
     __builtin_amdgcn_wave_barrier();
 #if defined(__HIP_DEVICE_COMPILE__)
     // LDS DMA (global_load_lds): each lane's 16 (or 4) bytes go straight to
@@ -970,18 +996,40 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const StagedBook sb{reinterpret_cast<uint16_t *>(slv), srec};
+    RowBuffer rb{rows, kStageRows, 0, 0};
+    if (lane == src) rb.base = sink.base;
+    // The owning lane runs until its market is done or its row buffer is
+    // full; then all 64 lanes write the rows out, coalesced.
+    bool done = false;
+    while (!done) {
+      int32_t fin = 0;
+      if (lane == src) fin = match_loop<W, STATS>(st, c, sb, rb, out, bulk, 0x7FFFFFFF) ? 1 : 0;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int32_t n = __shfl(rb.n, src);
+      const int64_t base = shfl_i64(rb.base, src);
+      done = __shfl(fin, src) != 0;
+      flush_rows(out, rows, n, base, pfm, b.C, lane, 64);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (lane == src) {
+        rb.base += n;
+        rb.n = 0;
+      }
+    }
+    // the staged book back to global memory, coalesced
+    for (int32_t j = lane; j < b.O; j += 64) grec[j] = srec[j];
+    for (int32_t j = lane; j < b.L; j += 64) glv[j] = slv[j];
     if (lane == src) {
-#if defined(__HIP_DEVICE_COMPILE__)
-      sink.lds = reinterpret_cast<int32_t *>(slv + b.L);
-      sink.lane = 0;
-      sink.stride = 1;
-#endif
-      const StagedBook sb{c.lv, c.rec, reinterpret_cast<uint16_t *>(slv), srec};
-      match_loop<W, STATS>(st, c, sb, sink, out, bulk, 0x7FFFFFFF);
-      quote_epilogue<W, STATS>(b, out, c, st, sink);
+      sink.base = rb.base;
+      quote_epilogue<W, STATS>(b, out, c, st, sink, sb);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
   write_bulk_wave(out, bulk);
 }
@@ -1037,6 +1085,7 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   (void)s;
   std::vector<uint4> srec(staged ? (size_t)h->O : 0);
   std::vector<uint16_t> slv(staged ? (size_t)h->L * 4 : 0);
+  std::vector<int32_t> rows((size_t)kStageRows * 8);
   for (int64_t m = 0; m < b.M; ++m) {
     Bulk bulk;
     bulk.count = 0;
@@ -1048,16 +1097,29 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
     const GlobalBook gb{c.lv, c.rec};
     const bool done = b.stats ? match_loop<W, true>(st, c, gb, sink, fo, bulk, budget)
                               : match_loop<W, false>(st, c, gb, sink, fo, bulk, budget);
-    if (!done) {  // the second pass, as on the GPU
+    if (done) {
+      if (b.stats) quote_epilogue<W, true>(b, fo, c, st, sink, gb);
+      else quote_epilogue<W, false>(b, fo, c, st, sink, gb);
+    } else {  // the second pass, as on the GPU
       sink.flush(fo, c.pf, c.C);
       std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
       std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
-      const StagedBook sb{c.lv, c.rec, slv.data(), srec.data()};
-      if (b.stats) match_loop<W, true>(st, c, sb, sink, fo, bulk, 0x7FFFFFFF);
-      else match_loop<W, false>(st, c, sb, sink, fo, bulk, 0x7FFFFFFF);
+      const StagedBook sb{slv.data(), srec.data()};
+      RowBuffer rb{rows.data(), kStageRows, 0, sink.base};
+      bool fin = false;
+      while (!fin) {
+        fin = b.stats ? match_loop<W, true>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF)
+                      : match_loop<W, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF);
+        flush_rows(fo, rows.data(), rb.n, rb.base, c.pf, c.C, 0, 1);
+        rb.base += rb.n;
+        rb.n = 0;
+      }
+      std::memcpy(c.rec, srec.data(), (size_t)h->O * 16);
+      std::memcpy(c.lv, slv.data(), (size_t)h->L * 8);
+      sink.base = rb.base;
+      if (b.stats) quote_epilogue<W, true>(b, fo, c, st, sink, sb);
+      else quote_epilogue<W, false>(b, fo, c, st, sink, sb);
     }
-    if (b.stats) quote_epilogue<W, true>(b, fo, c, st, sink);
-    else quote_epilogue<W, false>(b, fo, c, st, sink);
     if (bulk.count > 0) write_bulk_host(fo, bulk);
   }
 #else
