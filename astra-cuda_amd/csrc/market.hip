@@ -794,15 +794,9 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
                              const LoopState<W> &s, FillSink &sink, const BookMem &bk) {
   const int64_t M = b.M, m = c.m;
   const int32_t L = c.L, O = c.O;
-  sink.flush(out, c.pf, c.C);
-  out.counts[m] = s.fc;
-#pragma unroll
-  for (int i = 0; i < W; ++i) {
-    b.masks[(int64_t)i * M + m] = s.bm[i];
-    b.masks[(int64_t)(W + i) * M + m] = s.am[i];
-  }
-  b.next_slot[m] = c.ns;
-
+  // Loads first, then plain stores, then the fill rows and their portfolio
+  // atomics: the wait for a load also waits for every memory operation issued
+  // before it, and atomics are the slowest of those.
   int32_t obs = 0, oas = 0;
   if (s.bb >= 0 && s.bh < (uint32_t)O) {
     if (s.have_b) obs = (int32_t)s.brec.x;
@@ -816,10 +810,18 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
     else if (s.fc == 0 && s.ah == c.bslot) oas = (int32_t)c.krb.x;
     else oas = bk.size(s.ah);
   }
+  out.counts[m] = s.fc;
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    b.masks[(int64_t)i * M + m] = s.bm[i];
+    b.masks[(int64_t)(W + i) * M + m] = s.am[i];
+  }
+  b.next_slot[m] = c.ns;
   b.bbo[m] = (s.bb >= 0 && s.bh < (uint32_t)O) ? s.bb : ASTRA_NULL_INDEX;
   b.bbo[M + m] = obs;
   b.bbo[2 * M + m] = (s.ba < L && s.ah < (uint32_t)O) ? s.ba : ASTRA_NULL_INDEX;
   b.bbo[3 * M + m] = oas;
+  sink.flush(out, c.pf, c.C);
 
   if (STATS) {  // uniform addresses: the compiler aggregates these per wave
     add_u64(b.stats + 0, (unsigned long long)(c.bid_ok + c.ask_ok));
