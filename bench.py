@@ -12,7 +12,9 @@ pre-timed state, so they see exactly the same work):
   A  throughput: W warm-up steps, then exactly K steps, no host sync inside,
      bracketed by torch.cuda.synchronize() on both sides;
   B  latency: per-step host time with the stream synced (p50 / p99 / max);
-  C  device time: HIP events around every kernel launch (stream busy, async);
+  C  device time: HIP events on the launch stream around the K matching-kernel
+     launches issued back to back (then around K get_bbos launches), so the
+     mean per launch is the kernel's average duration;
   D  work counts: the diagnostic kernel variant counts inserts, fill rows and
      emptied levels, for the algorithmic-byte roofline.
 Then the CPU baseline: the oracle (a C port of the reference algorithm) on a
@@ -163,20 +165,25 @@ def main():
     lat_ms = np.array(lat) * 1e3
 
     # ---- C: device time per kernel (HIP events on the launch stream) ----
-    nev = K if "C" in phases else 0
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(nev)]
-    torch.cuda.synchronize()
-    for i, t in enumerate(range(W, W + nev)):
-        e = evs[i]
-        e[0].record()
-        snaps[1].add_two_sided_quotes(*rows[t], fills)
-        e[1].record()
+    # The matching kernel of the K timed steps, replayed back to back (get_bbos
+    # reads state only, so leaving it out changes no step), then K get_bbos.
+    qm_ms = np.array([wall / K * 1e3])
+    bbo_ms = np.zeros(1)
+    if "C" in phases:
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        torch.cuda.synchronize()
+        ev[0].record()
+        for t in range(W, T):
+            snaps[1].add_two_sided_quotes(*rows[t], fills)
+        ev[1].record()
         if bbo:
-            snaps[1].get_bbos(bbos)
-        e[2].record()
-    torch.cuda.synchronize()
-    qm_ms = np.array([e[0].elapsed_time(e[1]) for e in evs]) if nev else np.array([wall / K * 1e3])
-    bbo_ms = np.array([e[1].elapsed_time(e[2]) for e in evs]) if (bbo and nev) else np.zeros(1)
+            for t in range(W, T):
+                snaps[1].get_bbos(bbos)
+        ev[2].record()
+        torch.cuda.synchronize()
+        qm_ms = np.array([ev[0].elapsed_time(ev[1]) / K])
+        if bbo:
+            bbo_ms = np.array([ev[1].elapsed_time(ev[2]) / K])
 
     # ---- D: exact work counts for the algorithmic bytes ----
     counters = torch.zeros(8, dtype=torch.int64, device=dev)
@@ -196,6 +203,7 @@ def main():
     qm_avg_s = float(qm_ms.mean()) * 1e-3
     achieved = qm_bytes / qm_avg_s / 1e9
 
+    traffic, traffic_src = measured_traffic(cfg, M, bbo)
     value = M * K / wall
     result = {
         "metric": "quote-matches/sec and market-steps/sec at 100k markets; p50 step latency",
@@ -230,7 +238,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "algorithmic_bytes_per_launch": qm_bytes,
             "get_bbos_algorithmic_bytes_per_launch": bbo_bytes,
         },
@@ -240,6 +249,26 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, cfg, host, M, W, K, bbo)
     print(json.dumps(result), flush=True)
+
+
+def measured_traffic(cfg, M, bbo):
+    """HBM bytes per matching-kernel launch for this workload, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None."""
+    if M != cfg.M or bbo != cfg.bbo_every_step:
+        return None, None
+    words = 1
+    while words * 64 < cfg.L:
+        words *= 2
+    key = f"traffic_bytes_per_launch[void quote_match_kernel<{words}, false>]:"
+    path = os.path.join(ROOT, "profiles", f"quote_match_config{cfg.index}_{cfg.name}_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(key):
+                    return float(line.split(":", 1)[1]), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
 
 
 def cpu_baseline(args, cfg, host, M, W, K, bbo):
