@@ -494,6 +494,7 @@ struct LoopState {
 // on the GPU) that the loop reads and writes; it is copied back to global
 // memory when the market is done.
 struct GlobalBook {
+  static constexpr bool kStaged = false;
   uint16_t *lv;
   uint4 *rec;
   ASTRA_HD uint4 record(uint32_t s) const { return rec[s]; }
@@ -507,6 +508,7 @@ struct GlobalBook {
 };
 
 struct StagedBook {
+  static constexpr bool kStaged = true;
   uint16_t *slv;
   uint4 *srec;
   ASTRA_HD uint4 record(uint32_t s) const { return srec[s]; }
@@ -638,6 +640,53 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   s.emptied = s.forwarded = 0;
 }
 
+// The fill row of one pass (market.cu:172-218): the earlier TID rests (ties go
+// to the ask side); price, quote size and quote TID are the resting order's.
+ASTRA_HD void make_row(const uint4 &b, const uint4 &a, int32_t qty, int32_t (&row)[8]) {
+  const bool bid_quote = (int32_t)b.z < (int32_t)a.z;
+  row[0] = (int32_t)((bid_quote ? b.w : a.w) & kNull16);
+  row[1] = qty;
+  row[2] = (int32_t)(bid_quote ? a.y : b.y);
+  row[3] = (int32_t)(bid_quote ? b.y : a.y);
+  row[4] = bid_quote ? 0 : 1;
+  row[5] = (int32_t)(bid_quote ? b.x : a.x);
+  row[6] = (int32_t)(bid_quote ? a.z : b.z);
+  row[7] = (int32_t)(bid_quote ? b.z : a.z);
+}
+
+// Passes in which one side's head has size 0 and the other side's a positive
+// size: the fill is 0, nothing but that head changes, and it moves to the next
+// order of its level (:237-256). Runs such passes back to back while the next
+// order exists, differs from the current one and from the other head; writes
+// the level's head once at the end. Called at the top of a pass with both
+// records loaded; returns false when the budget or the sink stopped it (state
+// intact at the top of a pass).
+template <int SIDE, int W, class BookMem, class Sink>
+ASTRA_HD bool zero_walk(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, Sink &sink,
+                        const FillOut &out, int32_t budget, int32_t &passes) {
+  uint4 &w = SIDE == 0 ? s.brec : s.arec;
+  uint32_t &h = SIDE == 0 ? s.bh : s.ah;
+  const uint32_t start = h;
+  bool ok = true;
+  for (;;) {
+    const uint32_t nh = rec_next(w);
+    if (nh == kNull16 || nh == h || s.fc >= c.F) break;
+    int32_t row[8];
+    make_row(s.brec, s.arec, 0, row);
+    sink.put(out, c.pf, c.C, row);
+    ++s.fc;
+    h = nh;
+    w = bk.record(nh);
+    if (passes++ >= budget || sink.full()) {
+      ok = false;
+      break;
+    }
+    if ((int32_t)w.x != 0 || s.bh == s.ah) break;
+  }
+  if (h != start) bk.set_head(SIDE == 0 ? s.bb : s.ba, SIDE, h);
+  return ok;
+}
+
 // match_orders_kernel's crossing loop (market.cu:145-274). Runs at most
 // `budget` passes and stops early when the sink is full; returns false (state
 // intact, nothing of the next pass done) when it stopped before the end.
@@ -685,24 +734,23 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
       if (s.pa < L) s.paw = bk.word(s.pa, 1);
       s.ahead = true;
     }
+    // On the staged book a pass costs instructions, not memory round trips,
+    // so the short zero-size walk pays there (in global memory it does not).
+    if (BookMem::kStaged && s.bh != s.ah) {
+      if ((int32_t)s.brec.x == 0 && (int32_t)s.arec.x > 0) {
+        if (!zero_walk<0>(s, c, bk, sink, out, budget, passes)) return false;
+      } else if ((int32_t)s.arec.x == 0 && (int32_t)s.brec.x > 0) {
+        if (!zero_walk<1>(s, c, bk, sink, out, budget, passes)) return false;
+      }
+    }
     const int32_t bsz = (int32_t)s.brec.x, asz = (int32_t)s.arec.x;
-    const int32_t bcu = (int32_t)s.brec.y, acu = (int32_t)s.arec.y;
-    const int32_t btid = (int32_t)s.brec.z, atid = (int32_t)s.arec.z;
-    const bool bid_quote = btid < atid;  // earlier TID rests (:172)
-    const int32_t price = (int32_t)((bid_quote ? s.brec.w : s.arec.w) & kNull16);
     const int32_t qty = bsz < asz ? bsz : asz;
     if (s.fc >= F) {  // overflow sentinel (:187-195)
       s.fc = -1;
       break;
     }
-    const int32_t row[8] = {price,
-                            qty,
-                            bid_quote ? acu : bcu,
-                            bid_quote ? bcu : acu,
-                            bid_quote ? 0 : 1,
-                            bid_quote ? bsz : asz,
-                            bid_quote ? atid : btid,
-                            bid_quote ? btid : atid};
+    int32_t row[8];
+    make_row(s.brec, s.arec, qty, row);
     if (s.bh == s.ah && bsz != 0) {
       // One slot heads both sides with size s != 0: q = s, the slot becomes -s,
       // neither side pops, and the next pass is the same with -s. The fills
@@ -1254,7 +1302,7 @@ int default_stage_budget() {
     const int v = std::atoi(e);
     if (v >= 0) return v;
   }
-  return 16;
+  return 12;
 }
 
 int default_block() {
