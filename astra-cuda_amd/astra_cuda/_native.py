@@ -38,7 +38,34 @@ PROTOTYPES = {
     "astra_market_set_stats": (_c_int, [_vp, _vp]),
     "astra_market_get_tid": (_c_int, [_vp, ctypes.POINTER(_c_i32)]),
     "astra_market_set_tid": (_c_int, [_vp, _c_i32]),
+    "astra_market_shape": (_c_int, [_vp] + [ctypes.POINTER(_c_i32)] * 5),
+    "astra_market_bbo_cache": (_c_int, [_vp, ctypes.POINTER(_vp)]),
+    "astra_high_low_trade": (_c_int, [_vp, _vp, _vp]),
+    "astra_high_low_observation": (_c_int, [_vp, _vp]),
 }
+
+
+class HLTrade(ctypes.Structure):
+    """astra_hl_trade (include/astra_high_low.h)."""
+    _fields_ = [(n, _vp) for n in (
+        "move", "columns", "player_last_positions", "target_positions", "contract_values",
+        "player_contract_over_time", "market_contract_over_time", "immediate_rewards",
+        "rewards_since_last_action", "fill_prices", "fill_sizes", "fill_customer_ids",
+        "fill_quoter_ids", "fill_is_sell_quote", "fill_quote_sizes", "fill_tid", "fill_quote_tid",
+        "fill_counts", "best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes",
+        "last_prices", "errors")] + [(n, _c_i32) for n in (
+        "players", "steps_per_player", "max_contracts_per_trade", "max_contract_value", "player",
+        "trade_move_number", "check")]
+
+
+class HLObservation(ctypes.Structure):
+    """astra_hl_observation (include/astra_high_low.h)."""
+    _fields_ = [(n, _vp) for n in (
+        "values", "player_permutation", "contract_values", "contract_high_settle",
+        "target_positions", "player_contract_over_time", "best_bid_prices", "best_ask_prices",
+        "best_bid_sizes", "best_ask_sizes", "last_prices")] + [(n, _c_i32) for n in (
+        "num_envs", "players", "steps_per_player", "player", "current_round")] + [
+        (n, ctypes.c_float) for n in ("player_sin", "player_cos", "round_fraction")]
 
 _lib = None
 

@@ -1,5 +1,8 @@
 """Builds ``libastra_market.so`` (the HIP engine + C ABI) in-tree for gfx950.
 
+Sources: ``csrc/market.hip`` (the VecMarket engine, include/astra_market.h) and
+``csrc/high_low.hip`` (the high-low game's move kernels, include/astra_high_low.h).
+
 Usage: ``python astra-cuda_amd/astra_cuda/build.py`` or ``astra_cuda.build.build()``.
 The library links the HIP runtime by its SONAME (libamdhip64.so.7); imported after
 torch, it binds to the runtime torch already loaded, so both share streams.
@@ -17,6 +20,7 @@ CSRC = os.path.join(os.path.dirname(PKG_DIR), "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_NAME = "libastra_market.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+SOURCES = [os.path.join(CSRC, "market.hip"), os.path.join(CSRC, "high_low.hip")]
 
 ARCH = os.environ.get("ASTRA_OFFLOAD_ARCH", "gfx950")
 
@@ -41,10 +45,9 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile csrc/market.hip into the package directory. Always recompiles."""
-    src = os.path.join(CSRC, "market.hip")
+    """Compile the sources into the package directory. Always recompiles."""
     tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", src, "-o", tmp]
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", *SOURCES, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,0 +1,416 @@
+"""The high-low trading game on the MI355X engine.
+
+Mirrors nlyu1/astra-cuda src/games/high_low_trading/high_low_trading.{h,cc}
+(``HighLowTradingGame``, ``HighLowTradingState``) with the method names of the
+reference's core bindings (src/pybind/core/core_bindings.cc:33-115), so code
+written against ``astra.load_game("high_low_trading", params)`` runs unchanged.
+One state holds ``num_markets`` independent envs, each a VecMarket market.
+
+The trading move (ApplyPlayerTrading, high_low_trading.cc:247-329) and
+FillObservationTensor (:510-602) run as the HIP kernels of
+include/astra_high_low.h: three launches per move and one sync for the input
+checks (the reference makes eight); ``check_moves=False`` drops that sync, and
+``check_errors()`` then reports any move that failed a check. The chance moves
+(:136-226), rewards, returns and reset are the reference's tensor operations.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+from . import _native
+from .order_matching import VecMarket, _check, _fatal, _raw_stream
+
+MAX_CHANCE_NODES = 4            # high_low_trading.h:127-133
+CHANCE_PLAYER_ID = -1           # src/core/core.h kChancePlayerId
+TERMINAL_PLAYER_ID = -4         # src/core/core.h kTerminalPlayerId
+
+# high_low_trading.h:19-26 and the parameter specification (high_low_trading.cc:36-45)
+DEFAULT_PARAMETERS = {
+    "steps_per_player": 20,
+    "max_contracts_per_trade": 5,
+    "customer_max_size": 5,
+    "max_contract_value": 30,
+    "players": 5,
+    "num_markets": 32768,
+    "threads_per_block": 128,
+    "device_id": 0,
+}
+# Not in the reference: override the market shape the game derives (:57-69), for
+# game-shaped benchmarks on larger books. num_customers must be >= players.
+MARKET_SHAPE_PARAMETERS = ("market_price_levels", "market_orders", "market_fills", "market_customers")
+
+
+def _assert(cond: bool, what: str):
+    if not cond:
+        _fatal(f"high_low_trading.py {what}")
+
+
+class HighLowTradingGame:
+    """HighLowTradingGame (high_low_trading.h:117-153)."""
+
+    short_name = "high_low_trading"
+
+    def __init__(self, params: dict | None = None):
+        params = dict(params or {})
+        unknown = set(params) - set(DEFAULT_PARAMETERS) - set(MARKET_SHAPE_PARAMETERS) - {"check_moves"}
+        if unknown:
+            _fatal(f"Unknown parameter(s) for high_low_trading: {sorted(unknown)}")
+        self._params = {**DEFAULT_PARAMETERS, **params}
+        p = self._params
+        self.steps_per_player = int(p["steps_per_player"])
+        self.max_contracts_per_trade = int(p["max_contracts_per_trade"])
+        self.customer_max_size = int(p["customer_max_size"])
+        self.max_contract_value = int(p["max_contract_value"])
+        self.players = int(p["players"])
+        self.num_markets = int(p["num_markets"])
+        self.threads_per_block = int(p["threads_per_block"])
+        self.device_id = int(p["device_id"])
+        self.check_moves = bool(p.get("check_moves", True))
+        orders = self.players * self.steps_per_player * 2  # :57-69
+        self.market_shape = (
+            int(p.get("market_price_levels", self.max_contract_value + 1)),
+            int(p.get("market_orders", orders)),
+            int(p.get("market_fills", min(orders, self.max_contracts_per_trade * 2))),
+            int(p.get("market_customers", self.players)),
+        )
+        if self.market_shape[3] < self.players:
+            _fatal("high_low_trading.py market_customers >= players")
+
+    # core_bindings.cc:93-115
+    def new_initial_state(self) -> "HighLowTradingState":
+        return HighLowTradingState(self)
+
+    def get_parameters(self) -> dict:
+        return {k: v for k, v in self._params.items()}
+
+    def num_players(self) -> int:
+        return self.players
+
+    def max_chance_nodes_in_history(self) -> int:
+        return MAX_CHANCE_NODES
+
+    def max_game_length(self) -> int:  # high_low_trading.h:124-126
+        return MAX_CHANCE_NODES + self.steps_per_player * self.players
+
+    def max_move_number(self) -> int:
+        return self.max_game_length()
+
+    def observation_tensor_shape(self) -> list:  # :506-508
+        return [self.num_markets, 6 + 1 + 6 * self.players + 5]
+
+    def information_state_tensor_shape(self):  # :491-493
+        _fatal("InformationStateTensorShape not implemented")
+
+    NumPlayers = num_players
+    MaxGameLength = max_game_length
+    MaxChanceNodesInHistory = max_chance_nodes_in_history
+    ObservationTensorShape = observation_tensor_shape
+    NewInitialState = new_initial_state
+
+    def __repr__(self):
+        return f"high_low_trading({self._params})"
+
+
+class HighLowTradingState:
+    """HighLowTradingState (high_low_trading.h:30-115)."""
+
+    def __init__(self, game: HighLowTradingGame, _clone_of: "HighLowTradingState | None" = None):
+        self._game = game
+        N, P, T = game.num_markets, game.players, game.steps_per_player
+        self._N, self._P, self._T = N, P, T
+        self._dev = torch.device("cuda", game.device_id)
+        if _clone_of is None:
+            L, O, F, C = game.market_shape
+            ext = L > 128 or O > 1024 or F > 1024 or C > 1024
+            self.market = VecMarket(N, L, O, F, C, game.device_id, game.threads_per_block,
+                                    allow_extended_shapes=ext)
+            i32 = dict(dtype=torch.int32, device=self._dev)
+            self.contract_values = torch.zeros((N, 3), **i32)
+            self.contract_high_settle = torch.zeros((N,), dtype=torch.bool, device=self._dev)
+            self.player_permutation = torch.zeros((N, P), **i32)
+            self.inv_permutation = torch.zeros((N, P), **i32)
+            self.target_positions = torch.zeros((N, P), **i32)
+            self.player_last_positions = torch.zeros((N, P, 2), **i32)
+            self.player_contract_over_time = torch.zeros((N, P, T, 6), **i32)
+            self.market_contract_over_time = torch.zeros((N, P * T, 3), **i32)
+            self.immediate_rewards = torch.zeros((N, P), **i32)
+            self.rewards_since_last_action = torch.zeros((N, P), **i32)
+            self.bbo_batch = self.market.new_bbo_batch()
+            self.fill_batch = self.market.new_fill_batch()
+            self._move_number = 0
+        else:  # copy constructor (high_low_trading.cc:104-123)
+            o = _clone_of
+            self.market = o.market.clone()
+            for name in ("contract_values", "contract_high_settle", "player_permutation",
+                         "inv_permutation", "target_positions", "player_last_positions",
+                         "player_contract_over_time", "market_contract_over_time",
+                         "immediate_rewards", "rewards_since_last_action"):
+                setattr(self, name, getattr(o, name).clone())
+            self.bbo_batch = o.bbo_batch.clone()
+            self.fill_batch = o.fill_batch.clone()
+            self._move_number = o._move_number
+        self._columns = torch.empty((5, N), dtype=torch.int32, device=self._dev)
+        self._errors = torch.zeros((1,), dtype=torch.int32, device=self._dev)
+        self._lib = _native.lib()
+        self._trade = self._make_trade_args()
+
+    def _make_trade_args(self):
+        g = self._game
+        t = _native.HLTrade()
+        fb, bb = self.fill_batch, self.bbo_batch
+        ptrs = {
+            "columns": self._columns, "player_last_positions": self.player_last_positions,
+            "target_positions": self.target_positions, "contract_values": self.contract_values,
+            "player_contract_over_time": self.player_contract_over_time,
+            "market_contract_over_time": self.market_contract_over_time,
+            "immediate_rewards": self.immediate_rewards,
+            "rewards_since_last_action": self.rewards_since_last_action,
+            "errors": self._errors,
+        }
+        for f in ("fill_prices", "fill_sizes", "fill_customer_ids", "fill_quoter_ids", "fill_is_sell_quote",
+                  "fill_quote_sizes", "fill_tid", "fill_quote_tid", "fill_counts"):
+            ptrs[f] = getattr(fb, f)
+        for f in ("best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes", "last_prices"):
+            ptrs[f] = getattr(bb, f)
+        for k, v in ptrs.items():
+            assert v.is_contiguous() and v.device == self._dev, k
+            setattr(t, k, v.data_ptr())
+        t.players, t.steps_per_player = self._P, self._T
+        t.max_contracts_per_trade, t.max_contract_value = g.max_contracts_per_trade, g.max_contract_value
+        t.check = 1 if g.check_moves else 0
+        return t
+
+    # ---- core State (src/core/core.h, core.cc:15-20) ----
+    def current_player(self) -> int:  # :125-134
+        if self.is_terminal():
+            return TERMINAL_PLAYER_ID
+        if self._move_number < MAX_CHANCE_NODES:
+            return CHANCE_PLAYER_ID
+        return (self._move_number - MAX_CHANCE_NODES) % self._P
+
+    def is_terminal(self) -> bool:  # :465-467
+        return self._move_number >= self._game.max_game_length()
+
+    def is_chance_node(self) -> bool:
+        return self.current_player() == CHANCE_PLAYER_ID
+
+    def is_player_node(self) -> bool:
+        return self.current_player() >= 0
+
+    def is_simultaneous_node(self) -> bool:
+        return False
+
+    def is_player_acting(self, player: int) -> bool:
+        return self.current_player() == player
+
+    def move_number(self) -> int:
+        return self._move_number
+
+    def is_initial_state(self) -> bool:
+        return self._move_number == 0
+
+    def num_players(self) -> int:
+        return self._P
+
+    def get_game(self) -> HighLowTradingGame:
+        return self._game
+
+    def apply_action(self, action_id: torch.Tensor) -> int:
+        """ApplyAction (core.cc:15-20) -> DoApplyAction (:228-245)."""
+        player = self.current_player()
+        move = action_id
+        _assert(move.size(0) == self._N, f"move.size(0) == num_envs_\nmove.size(0) = {move.size(0)}, "
+                                         f"num_envs_ = {self._N}")
+        mn = self._move_number
+        if mn == 0:
+            self._apply_candidate_values(move)
+        elif mn == 1:
+            self._apply_high_low_settle(move)
+        elif mn == 2:
+            self._apply_permutation(move)
+        elif mn == 3:
+            self._apply_customer_size(move)
+        else:
+            self._apply_player_trading(move)
+        self._move_number += 1
+        return player
+
+    def child(self, action):
+        c = self.clone()
+        c.apply_action(action)
+        return c
+
+    def clone(self) -> "HighLowTradingState":
+        return HighLowTradingState(self._game, _clone_of=self)
+
+    def reset(self) -> None:
+        """Reset (core.h:427) -> DoReset (:375-394)."""
+        self._move_number = 0
+        for t in (self.contract_values, self.contract_high_settle, self.player_permutation,
+                  self.inv_permutation, self.target_positions, self.player_last_positions,
+                  self.player_contract_over_time, self.market_contract_over_time,
+                  self.immediate_rewards, self.rewards_since_last_action):
+            t.zero_()
+        self.market.reset()
+        self.bbo_batch.reset()
+        self.fill_batch.reset()
+
+    # ---- chance moves (:136-226), tensor operations as in the reference ----
+    def _apply_candidate_values(self, move):
+        _assert(move.dim() == 2, f"move.dim() == 2\nmove.dim() = {move.dim()}")
+        _assert(move.size(1) == 2, f"move.size(1) == 2\nmove.size(1) = {move.size(1)}")
+        lo, hi = int(torch.min(move).item()), int(torch.max(move).item())
+        _assert(lo >= 1, f"min_val >= 1\nmin_val = {lo}")
+        _assert(hi <= self._game.max_contract_value, f"max_val <= GetGame()->GetMaxContractValue()\nmax_val = {hi}")
+        self.contract_values[:, 0:2] = move
+
+    def _apply_high_low_settle(self, move):
+        _assert(move.dim() == 1, f"move.dim() == 1\nmove.dim() = {move.dim()}")
+        lo, hi = int(torch.min(move).item()), int(torch.max(move).item())
+        _assert(lo >= 0, f"min_val >= 0\nmin_val = {lo}")
+        _assert(hi <= 1, f"max_val <= 1\nmax_val = {hi}")
+        self.contract_high_settle.copy_(move.to(torch.bool))
+        mx = torch.max(self.contract_values[:, 0], self.contract_values[:, 1])
+        mn = torch.min(self.contract_values[:, 0], self.contract_values[:, 1])
+        self.contract_values[:, 2] = move * mx + (1 - move) * mn
+
+    def _apply_permutation(self, move):
+        _assert(move.dim() == 2, f"move.dim() == 2\nmove.dim() = {move.dim()}")
+        _assert(move.size(1) == self._P, f"move.size(1) == num_players_\nmove.size(1) = {move.size(1)}")
+        lo, hi = int(torch.min(move).item()), int(torch.max(move).item())
+        _assert(lo >= 0, f"min_val >= 0\nmin_val = {lo}")
+        _assert(hi < self._P, f"max_val < num_players_\nmax_val = {hi}")
+        self.player_permutation.copy_(move)
+        self.inv_permutation.copy_(move.argsort(dim=1))
+
+    def _apply_customer_size(self, move):
+        _assert(move.dim() == 2, f"move.dim() == 2\nmove.dim() = {move.dim()}")
+        _assert(move.size(1) == self._P - 3, f"move.size(1) == num_players_ - 3\nmove.size(1) = {move.size(1)}")
+        a = torch.abs(move)
+        _assert(int(torch.max(a).item()) <= self._game.customer_max_size,
+                "torch::max(abs_move).item<int>() <= GetGame()->GetCustomerMaxSize()")
+        _assert(int(torch.min(a).item()) > 0, "torch::min(abs_move).item<int>() > 0")
+        idx = self.inv_permutation[:, 3:]
+        self.target_positions.scatter_(1, idx.to(torch.int64), move.to(self.target_positions.dtype))
+
+    # ---- the trading move (:247-329) on the HIP kernels ----
+    def _apply_player_trading(self, move):
+        player = self.current_player()
+        tmn = self._move_number - MAX_CHANCE_NODES
+        _assert(move.dim() == 2 and move.size(1) == 4, f"move.size(1) == 4\nmove.size(1) = {move.size(-1)}")
+        if move.dtype != torch.int32:
+            _fatal(f"move tensor must be int32, got {move.dtype}")
+        if move.device != self._dev:
+            _fatal(f"move tensor must be on device {self._game.device_id}")
+        move = move.contiguous()
+        t = self._trade
+        t.move = move.data_ptr()
+        t.player = player
+        t.trade_move_number = tmn
+        rc = self._lib.astra_high_low_trade(self.market._h, ctypes.byref(t),
+                                           _raw_stream(self._game.device_id))
+        self._last_move = move  # keep the buffer alive while the kernels may read it
+        if rc:
+            self._errors.zero_()
+            _fatal(_native.last_error())
+
+    def check_errors(self) -> None:
+        """With check_moves=False: raise if any move since the last call failed the
+        reference's input checks (high_low_trading.cc:264-271). Synchronises."""
+        bits = int(self._errors.item())
+        if bits:
+            self._errors.zero_()
+            names = ("bid_prices > 0", "ask_prices > 0", "bid_prices <= max_contract_value",
+                     "ask_prices <= max_contract_value", "bid_sizes >= 0", "ask_sizes >= 0",
+                     "bid_sizes <= max_contracts_per_trade", "ask_sizes <= max_contracts_per_trade")
+            _fatal("high_low_trading.py moves failed: " + ", ".join(n for i, n in enumerate(names) if bits >> i & 1))
+
+    # ---- rewards and returns (:331-373) ----
+    def fill_rewards(self, reward_buffer: torch.Tensor) -> None:
+        _assert(reward_buffer.dim() == 2 and reward_buffer.size(0) == self._N and reward_buffer.size(1) == self._P,
+                "reward_buffer shape == [num_envs, num_players]")
+        reward_buffer.copy_(self.immediate_rewards)
+
+    def fill_rewards_since_last_action(self, reward_buffer: torch.Tensor, player_id: int) -> None:
+        _assert(reward_buffer.dim() == 1 and reward_buffer.size(0) == self._N,
+                "reward_buffer shape == [num_envs]")
+        reward_buffer.copy_(self.rewards_since_last_action[:, player_id])
+
+    def fill_returns(self, returns_buffer: torch.Tensor) -> None:
+        _assert(returns_buffer.dim() == 2 and returns_buffer.size(0) == self._N and returns_buffer.size(1) == self._P,
+                "returns_buffer shape == [num_envs, num_players]")
+        returns_buffer.zero_()
+        is_customer = self.target_positions != 0
+        pf = self.market.get_customer_portfolios()[:, :self._P]
+        returns_buffer.add_(pf[:, :, 1])
+        returns_buffer.addcmul_(pf[:, :, 0], self.contract_values[:, 2].unsqueeze(-1))
+        diff = torch.abs(pf[:, :, 0] - self.target_positions)
+        returns_buffer.add_(-is_customer.to(torch.int32) * diff * self._game.max_contract_value)
+
+    # ---- FillObservationTensor (:510-602) on the HIP kernel ----
+    def fill_observation_tensor(self, *args):
+        """fill_observation_tensor(player, values) or fill_observation_tensor(values) -> player
+        (core_bindings.cc:77-82)."""
+        if len(args) == 1:
+            values, player, ret = args[0], self.current_player(), True
+        else:
+            player, values = args
+            ret = False
+        g = self._game
+        _assert(0 <= player < self._P, f"player >= 0 && player < NumPlayers()\nplayer = {player}")
+        _assert(self._move_number >= MAX_CHANCE_NODES, "MoveNumber() >= MaxChanceNodesInHistory()")
+        shape = g.observation_tensor_shape()
+        _assert(list(values.shape) == shape, f"values.sizes() == {shape}\nvalues.sizes() = {list(values.shape)}")
+        if values.dtype != torch.float32 or not values.is_contiguous() or values.device != self._dev:
+            _fatal("values must be a contiguous float32 tensor on the game's device")
+        ctm = max(0, self._move_number - MAX_CHANCE_NODES)
+        cr = ctm // self._P
+        _assert(cr < self._T, f"current_round < steps_per_player\ncurrent_round = {cr}")
+        angle = 2.0 * math.pi * player / self._P
+        o = _native.HLObservation()
+        o.values = values.data_ptr()
+        o.player_permutation = self.player_permutation.data_ptr()
+        o.contract_values = self.contract_values.data_ptr()
+        o.contract_high_settle = self.contract_high_settle.data_ptr()
+        o.target_positions = self.target_positions.data_ptr()
+        o.player_contract_over_time = self.player_contract_over_time.data_ptr()
+        bb = self.bbo_batch
+        o.best_bid_prices = bb.best_bid_prices.data_ptr()
+        o.best_ask_prices = bb.best_ask_prices.data_ptr()
+        o.best_bid_sizes = bb.best_bid_sizes.data_ptr()
+        o.best_ask_sizes = bb.best_ask_sizes.data_ptr()
+        o.last_prices = bb.last_prices.data_ptr()
+        o.num_envs, o.players, o.steps_per_player = self._N, self._P, self._T
+        o.player, o.current_round = player, cr
+        o.player_sin = float(np.float32(math.sin(angle)))
+        o.player_cos = float(np.float32(math.cos(angle)))
+        o.round_fraction = float(np.float32(cr) / np.float32(self._T))
+        _check(self._lib.astra_high_low_observation(ctypes.byref(o), _raw_stream(g.device_id)))
+        return player if ret else None
+
+    def expose_info(self) -> dict:  # :475-485
+        if not self.is_terminal():
+            _fatal("ExposeInfo called on non-terminal state")
+        return {"players": self.player_contract_over_time.clone(),
+                "market": self.market_contract_over_time.clone(),
+                "target_positions": self.target_positions.clone()}
+
+    def get_contract_value(self) -> torch.Tensor:  # :469-473
+        _assert(self._move_number >= 2, "MoveNumber() >= 2")
+        return self.contract_values[:, 2]
+
+    # C++ method names
+    CurrentPlayer = current_player
+    IsTerminal = is_terminal
+    ApplyAction = apply_action
+    MoveNumber = move_number
+    FillRewards = fill_rewards
+    FillRewardsSinceLastAction = fill_rewards_since_last_action
+    FillReturns = fill_returns
+    FillObservationTensor = fill_observation_tensor
+    Clone = clone
+    Reset = reset

@@ -39,8 +39,6 @@
 // wrapper. Built with -DASTRA_HOST_EMULATION (host-only compile), the same
 // bodies run in plain loops over host memory behind the same C ABI; the tests
 // use that build to check the logic and its bounds on the CPU.
-#include <hip/hip_runtime.h>
-
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
@@ -48,84 +46,15 @@
 #include <string>
 #include <vector>
 
-#include "astra_market.h"
+#define ASTRA_SRC_NAME "market.hip"
+#include "runtime.h"
 
-#define ASTRA_HD __host__ __device__ __forceinline__
+using namespace astra_rt;
 
 namespace {
 
 constexpr uint32_t kNull16 = 0xFFFFu;
 constexpr int kFillThreads = 256;
-
-thread_local std::string g_last_error;
-
-int fail(int code, const std::string &msg) {
-  g_last_error = msg;
-  return code;
-}
-
-// Mirrors ASTRA_CHECK_OP's text (src/utils/astra_utils.h:116-131).
-#define ASTRA_ABI_CHECK(x_exp, op, y_exp)                                               \
-  do {                                                                                  \
-    long long x_ = (long long)(x_exp), y_ = (long long)(y_exp);                         \
-    if (!(x_ op y_))                                                                    \
-      return fail(ASTRA_ERR_INVALID_ARGUMENT,                                           \
-                  std::string("market.hip:") + std::to_string(__LINE__) + " " #x_exp    \
-                      " " #op " " #y_exp "\n" #x_exp " = " + std::to_string(x_) +       \
-                      ", " #y_exp " = " + std::to_string(y_));                          \
-  } while (false)
-
-#define ASTRA_HIP_CHECK(call, what)                                                     \
-  do {                                                                                  \
-    hipError_t e_ = (call);                                                             \
-    if (e_ != hipSuccess)                                                               \
-      return fail(ASTRA_ERR_HIP, std::string("HIP error in ") + (what) + ": " +         \
-                                     hipGetErrorString(e_));                           \
-  } while (false)
-
-// ---- runtime shims: the device build calls HIP, the emulation build works on
-// host memory ----
-#ifdef ASTRA_HOST_EMULATION
-hipError_t rt_device_count(int *n) {
-  *n = 1;
-  return hipSuccess;
-}
-hipError_t rt_memcpy(void *d, const void *s, size_t n, hipStream_t) {
-  std::memmove(d, s, n);
-  return hipSuccess;
-}
-hipError_t rt_sync(hipStream_t) { return hipSuccess; }
-hipError_t rt_last_error() { return hipSuccess; }
-struct DeviceGuard {
-  bool ok = true;
-  explicit DeviceGuard(int) {}
-};
-void rt_device_sync(int) {}
-#else
-hipError_t rt_device_count(int *n) { return hipGetDeviceCount(n); }
-hipError_t rt_memcpy(void *d, const void *s, size_t n, hipStream_t st) {
-  return hipMemcpyAsync(d, s, n, hipMemcpyDefault, st);
-}
-hipError_t rt_sync(hipStream_t st) { return hipStreamSynchronize(st); }
-hipError_t rt_last_error() { return hipGetLastError(); }
-// Restores the calling thread's current device when it goes out of scope.
-struct DeviceGuard {
-  int prev = -1;
-  bool ok = true;
-  explicit DeviceGuard(int dev) {
-    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-    if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
-  }
-  ~DeviceGuard() {
-    int cur = -1;
-    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-  }
-};
-void rt_device_sync(int dev) {
-  DeviceGuard g(dev);
-  (void)hipDeviceSynchronize();
-}
-#endif
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -141,7 +70,7 @@ inline int mask_words_for(int32_t L) {
 // Byte offsets of the book arrays inside the workspace.
 struct Layout {
   int W;
-  size_t masks, next_slot, bbo, levels, records, portfolios, total;
+  size_t masks, next_slot, bbo, tob, levels, records, portfolios, total;
 };
 
 Layout make_layout(int64_t M, int64_t L, int64_t O, int64_t C) {
@@ -154,6 +83,8 @@ Layout make_layout(int64_t M, int64_t L, int64_t O, int64_t C) {
   off = align_up(off + (size_t)M * 4, 256);
   l.bbo = off;
   off = align_up(off + (size_t)4 * M * 4, 256);
+  l.tob = off;
+  off = align_up(off + (size_t)M * 4, 256);
   l.levels = off;
   off = align_up(off + (size_t)M * L * 8, 256);
   l.records = off;
@@ -186,6 +117,7 @@ struct Book {
   uint64_t *masks;            // [2][W][M]: side 0 = bid, 1 = ask
   int32_t *next_slot;         // [M], in [0, O)
   int32_t *bbo;               // [4][M]: best bid price, size, best ask price, size
+  uint32_t *tob;              // [M]: head slots of the best levels, bid | ask << 16
   uint16_t *levels;           // [M][L][4] = {bid_head, bid_tail, ask_head, ask_tail}
   uint4 *records;             // [M][O] = {size, customer, tid, price | next << 16}
   int32_t *portfolios;        // [M][C][2] = {contracts, cash}
@@ -198,6 +130,7 @@ Book book_of(const astra_market *h) {
   b.masks = reinterpret_cast<uint64_t *>(h->ws + h->lay.masks);
   b.next_slot = reinterpret_cast<int32_t *>(h->ws + h->lay.next_slot);
   b.bbo = reinterpret_cast<int32_t *>(h->ws + h->lay.bbo);
+  b.tob = reinterpret_cast<uint32_t *>(h->ws + h->lay.tob);
   b.levels = reinterpret_cast<uint16_t *>(h->ws + h->lay.levels);
   b.records = reinterpret_cast<uint4 *>(h->ws + h->lay.records);
   b.portfolios = reinterpret_cast<int32_t *>(h->ws + h->lay.portfolios);
@@ -468,8 +401,6 @@ struct MarketCtx {
   uint16_t *lv;  // the market's level words and order records in global memory
   uint4 *rec;
   int32_t *pf;
-  uint32_t bslot, aslot;  // slots the two inserts took (0xFFFFFFFF if none)
-  uint4 krb, kra;         // their records as stored, next fields included
   int32_t ns;             // ring position after the inserts
   bool bid_ok, ask_ok;
 };
@@ -524,11 +455,18 @@ struct StagedBook {
 };
 
 // add_orders_kernel (market.cu:17-100) for market m and the set-up of the
-// matching loop: masks, the inserts, and the heads of the best levels.
+// matching loop (:122-142): masks, the inserts, the heads of the best levels
+// and their records.
 //
-// Memory round trips are what a lane waits on, so the two insert levels and
-// the two current best levels are read in one round trip, and the heads at
-// loop entry come from those words.
+// A lane waits on memory round trips, so the prologue takes two. The first
+// reads the market's coalesced words: quotes, masks, ring position, and the
+// head slots and head sizes of the best levels as the last call left them
+// (tob, BBO cache). That fixes the best levels after the inserts and whether
+// the book crosses. The second reads the two insert levels' words and, for a
+// market that crosses, the two head records and the next level of each side,
+// all at once, before the inserts write anything; the values are then patched
+// for what the inserts wrote (a slot the ring reuses, a tail link), so the
+// first loop pass starts with everything in registers.
 template <int W>
 ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, MarketCtx &c,
                              LoopState<W> &s) {
@@ -545,6 +483,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   uint16_t *lv = c.lv;
   uint4 *rec = c.rec;
 
+  // ---- round trip 1 ----
   const int32_t bid_px = in.bid_px[m], bid_sz = in.bid_sz[m];
   const int32_t ask_px = in.ask_px[m], ask_sz = in.ask_sz[m];
   const int32_t cust = in.cust[m];
@@ -554,23 +493,49 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
     s.am[i] = b.masks[(int64_t)(W + i) * M + m];
   }
   int32_t ns = b.next_slot[m];
+  const uint32_t tob = b.tob[m];
+  const int32_t bsz0 = b.bbo[M + m], asz0 = b.bbo[3 * M + m];
 
   const bool bid_ok = bid_sz > 0 && (uint32_t)bid_px < (uint32_t)L;
   const bool ask_ok = ask_sz > 0 && (uint32_t)ask_px < (uint32_t)L;
   const int bb0 = mask_highest<W>(s.bm);
   const int ba0 = mask_lowest<W>(s.am, L);
-  // One round trip for the four level words this call may start from. The bid
-  // insert only writes bid halves of level words, so the ask words read here
-  // are the ones the ask insert would have read after it.
+  // An insert above the best bid (below the best ask) lands on an empty level
+  // and becomes that side's best level with the new order as head.
+  const bool bid_top = bid_ok && bid_px > bb0;
+  const bool ask_top = ask_ok && ask_px < ba0;
+  const int bb = bid_top ? bid_px : bb0;
+  const int ba = ask_top ? ask_px : ba0;
+  const bool cross = bb >= 0 && ba < L && bb >= ba;
+  const uint32_t hb0 = tob & kNull16, ha0 = tob >> 16;
+
+  // ---- round trip 2 ----
   const uint32_t bword = bid_ok ? level_word(lv, bid_px, 0) : 0u;
   const uint32_t aword = ask_ok ? level_word(lv, ask_px, 1) : 0u;
-  const uint32_t bbw0 = bb0 >= 0 ? level_word(lv, bb0, 0) : 0xFFFFFFFFu;
-  const uint32_t baw0 = ba0 < L ? level_word(lv, ba0, 1) : 0xFFFFFFFFu;
+  uint4 hrb = make_uint4((uint32_t)bsz0, 0, 0, 0), hra = make_uint4((uint32_t)asz0, 0, 0, 0);
+  if (cross && !bid_top && hb0 < (uint32_t)O) hrb = rec[hb0];
+  if (cross && !ask_top && ha0 < (uint32_t)O) hra = rec[ha0];
+  int pb = -1, pa = L;
+  uint32_t pbw = 0xFFFFFFFFu, paw = 0xFFFFFFFFu;
+  if (cross) {
+    uint64_t t[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) t[i] = s.bm[i];
+    if (bid_ok) mask_set<W>(t, bid_px);
+    mask_clear<W>(t, bb);
+    pb = mask_highest<W>(t);
+    if (pb >= 0) pbw = level_word(lv, pb, 0);
+#pragma unroll
+    for (int i = 0; i < W; ++i) t[i] = s.am[i];
+    if (ask_ok) mask_set<W>(t, ask_px);
+    mask_clear<W>(t, ba);
+    pa = mask_lowest<W>(t, L);
+    if (pa < L) paw = level_word(lv, pa, 1);
+  }
 
   // ---- add: bid first, then ask (market.cu:44-70, 73-99) ----
-  // krb / kra track the two inserted records as stored, including later writes
-  // of their next fields, so the first match pass can use them unread.
   uint32_t bslot = 0xFFFFFFFFu, aslot = 0xFFFFFFFFu;
+  uint32_t btail = 0xFFFFFFFFu, atail = 0xFFFFFFFFu;  // old tails the inserts linked from
   uint4 krb = make_uint4(0, 0, 0, 0), kra = make_uint4(0, 0, 0, 0);
   if (bid_ok) {
     bslot = (uint32_t)ns;
@@ -586,7 +551,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
       lv[(size_t)bid_px * 4 + 1] = (uint16_t)bslot;
       if (old_tail < (uint32_t)O) {
         reinterpret_cast<uint16_t *>(rec + old_tail)[7] = (uint16_t)bslot;
-        if (old_tail == bslot) krb = with_next(krb, bslot);
+        btail = old_tail;
       }
     }
   }
@@ -596,7 +561,6 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
     kra = make_uint4((uint32_t)ask_sz, (uint32_t)cust, (uint32_t)((uint32_t)in.base_tid + 1u),
                      (uint32_t)ask_px | (kNull16 << 16));
     rec[aslot] = kra;
-    if (aslot == bslot) krb = kra;  // O == 1: the ask reused the bid's slot
     const uint32_t old_tail = aword >> 16;
     if (old_tail == kNull16) {
       store_level_word(lv, ask_px, 1, aslot | (aslot << 16));
@@ -605,37 +569,48 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
       lv[(size_t)ask_px * 4 + 3] = (uint16_t)aslot;
       if (old_tail < (uint32_t)O) {
         reinterpret_cast<uint16_t *>(rec + old_tail)[7] = (uint16_t)aslot;
-        if (old_tail == bslot) krb = with_next(krb, aslot);
-        if (old_tail == aslot) kra = with_next(kra, aslot);
+        atail = old_tail;
       }
     }
   }
-  c.bslot = bslot;
-  c.aslot = aslot;
-  c.krb = krb;
-  c.kra = kra;
+  // A record read before the inserts, as the inserts left it: the bid record
+  // overwrites its slot, the bid links its old tail to it, then the same for
+  // the ask (a slot can be both, e.g. O == 1).
+  auto patched = [&](uint32_t slot, uint4 r) {
+    if (slot == bslot) r = krb;
+    if (slot == btail) r = with_next(r, bslot);
+    if (slot == aslot) r = kra;
+    if (slot == atail) r = with_next(r, aslot);
+    return r;
+  };
   c.ns = ns;
   c.bid_ok = bid_ok;
   c.ask_ok = ask_ok;
 
-  // ---- heads of the best levels, known without another read ----
-  s.bb = mask_highest<W>(s.bm);
-  s.ba = mask_lowest<W>(s.am, L);
-  s.bh = kNull16;
-  s.ah = kNull16;
-  if (s.bb >= 0)
-    s.bh = (bid_ok && s.bb == bid_px) ? ((bword >> 16) == kNull16 ? bslot : (bword & kNull16))
-                                      : (bbw0 & kNull16);
-  if (s.ba < L)
-    s.ah = (ask_ok && s.ba == ask_px) ? ((aword >> 16) == kNull16 ? aslot : (aword & kNull16))
-                                      : (baw0 & kNull16);
-  s.brec = make_uint4(0, 0, 0, 0);
-  s.arec = make_uint4(0, 0, 0, 0);
-  s.have_b = s.have_a = false;
-  s.pb = -1;
-  s.pa = L;
-  s.pbw = s.paw = 0xFFFFFFFFu;
-  s.ahead = false;
+  // ---- the matching loop's entry state ----
+  // For a market that does not cross only the head sizes are used (by the
+  // BBO); they come from the BBO cache unless an insert rewrote the slot.
+  s.bb = bb;
+  s.ba = ba;
+  s.bh = s.ah = kNull16;
+  s.brec = s.arec = make_uint4(0, 0, 0, 0);
+  if (bb >= 0) {
+    s.bh = bid_top ? bslot : hb0;
+    s.brec = patched(s.bh, hrb);
+  }
+  if (ba < L) {
+    s.ah = ask_top ? aslot : ha0;
+    s.arec = patched(s.ah, hra);
+  }
+  s.have_b = s.have_a = true;
+  // the next levels read ahead, as the inserts left their heads
+  if (bid_ok && pb == bid_px && (bword >> 16) == kNull16) pbw = bslot | (bslot << 16);
+  if (ask_ok && pa == ask_px && (aword >> 16) == kNull16) paw = aslot | (aslot << 16);
+  s.pb = pb;
+  s.pa = pa;
+  s.pbw = pbw;
+  s.paw = paw;
+  s.ahead = cross;
   s.fc = 0;
   s.emptied = s.forwarded = 0;
 }
@@ -705,19 +680,14 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
   while (s.bb >= 0 && s.ba < L && s.bb >= s.ba) {
     if (s.bh >= (uint32_t)O || s.ah >= (uint32_t)O) break;  // NULL head (:155)
     if (passes++ >= budget || sink.full()) return false;
-    // Records: before the first fill nothing has changed, so the inserted
-    // records come from registers; after that every size change has been
-    // written through, so memory is current.
+    // Records of heads that changed (the entry heads come from the prologue);
+    // every size change is written through, so memory is current.
     if (!s.have_b) {
-      if (s.fc == 0 && s.bh == c.aslot) s.brec = c.kra;
-      else if (s.fc == 0 && s.bh == c.bslot) s.brec = c.krb;
-      else s.brec = bk.record(s.bh);
+      s.brec = bk.record(s.bh);
       s.have_b = true;
     }
     if (!s.have_a) {
-      if (s.fc == 0 && s.ah == c.aslot) s.arec = c.kra;
-      else if (s.fc == 0 && s.ah == c.bslot) s.arec = c.krb;
-      else s.arec = bk.record(s.ah);
+      s.arec = bk.record(s.ah);
       s.have_a = true;
     }
     if (!s.ahead) {  // read the next level of each side ahead
@@ -842,22 +812,12 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
                              const LoopState<W> &s, FillSink &sink, const BookMem &bk) {
   const int64_t M = b.M, m = c.m;
   const int32_t L = c.L, O = c.O;
-  // Loads first, then plain stores, then the fill rows and their portfolio
-  // atomics: the wait for a load also waits for every memory operation issued
-  // before it, and atomics are the slowest of those.
+  // Loads first, then plain stores and the fill rows with their portfolio
+  // atomics, then the stores that need the loaded values: the wait for a load
+  // also waits for every memory operation issued before it.
   int32_t obs = 0, oas = 0;
-  if (s.bb >= 0 && s.bh < (uint32_t)O) {
-    if (s.have_b) obs = (int32_t)s.brec.x;
-    else if (s.fc == 0 && s.bh == c.aslot) obs = (int32_t)c.kra.x;
-    else if (s.fc == 0 && s.bh == c.bslot) obs = (int32_t)c.krb.x;
-    else obs = bk.size(s.bh);
-  }
-  if (s.ba < L && s.ah < (uint32_t)O) {
-    if (s.have_a) oas = (int32_t)s.arec.x;
-    else if (s.fc == 0 && s.ah == c.aslot) oas = (int32_t)c.kra.x;
-    else if (s.fc == 0 && s.ah == c.bslot) oas = (int32_t)c.krb.x;
-    else oas = bk.size(s.ah);
-  }
+  if (s.bb >= 0 && s.bh < (uint32_t)O) obs = s.have_b ? (int32_t)s.brec.x : bk.size(s.bh);
+  if (s.ba < L && s.ah < (uint32_t)O) oas = s.have_a ? (int32_t)s.arec.x : bk.size(s.ah);
   out.counts[m] = s.fc;
 #pragma unroll
   for (int i = 0; i < W; ++i) {
@@ -865,11 +825,12 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
     b.masks[(int64_t)(W + i) * M + m] = s.am[i];
   }
   b.next_slot[m] = c.ns;
+  sink.flush(out, c.pf, c.C);  // overlaps the loads above
   b.bbo[m] = (s.bb >= 0 && s.bh < (uint32_t)O) ? s.bb : ASTRA_NULL_INDEX;
   b.bbo[M + m] = obs;
   b.bbo[2 * M + m] = (s.ba < L && s.ah < (uint32_t)O) ? s.ba : ASTRA_NULL_INDEX;
   b.bbo[3 * M + m] = oas;
-  sink.flush(out, c.pf, c.C);
+  b.tob[m] = ((s.bb >= 0 ? s.bh : kNull16) & kNull16) | ((s.ba < L ? s.ah : kNull16) << 16);
 
   if (STATS) {  // uniform addresses: the compiler aggregates these per wave
     add_u64(b.stats + 0, (unsigned long long)(c.bid_ok + c.ask_ok));
@@ -922,6 +883,7 @@ ASTRA_HD void clear_quotes_thread(const Book &b, const uint8_t *reset, int64_t t
     b.bbo[M + m] = 0;
     b.bbo[2 * M + m] = ASTRA_NULL_INDEX;
     b.bbo[3 * M + m] = 0;
+    b.tob[m] = 0xFFFFFFFFu;
   }
 }
 
@@ -1118,8 +1080,6 @@ __global__ __launch_bounds__(kFillThreads) void fill_u32_kernel(uint32_t *dst, i
 
 // ---- launchers (kernel on the device build, host loop on the emulation build) ----
 
-hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
-
 inline unsigned grid_for(int64_t n, int block) { return (unsigned)((n + block - 1) / block); }
 
 template <int W>
@@ -1269,6 +1229,7 @@ int init_book(astra_market *h, hipStream_t s) {
   if ((rc = launch_fill(bbo + h->M, h->M, 0u, s, "init"))) return rc;
   if ((rc = launch_fill(bbo + 2 * (int64_t)h->M, h->M, 0xFFFFFFFFu, s, "init"))) return rc;
   if ((rc = launch_fill(bbo + 3 * (int64_t)h->M, h->M, 0u, s, "init"))) return rc;
+  if ((rc = launch_fill(h->ws + l.tob, h->M, 0xFFFFFFFFu, s, "init"))) return rc;
   if ((rc = launch_fill(h->ws + l.levels, (int64_t)h->M * h->L * 2, 0xFFFFFFFFu, s, "init")))
     return rc;
   return launch_fill(h->ws + l.portfolios, (int64_t)h->M * h->C * 2, 0u, s, "init");
@@ -1495,6 +1456,23 @@ int astra_market_clear_quotes(astra_market *h, const uint8_t *reset, void *strea
 int astra_market_portfolios(const astra_market *h, int32_t **p) {
   if (!h || !p) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL argument");
   *p = reinterpret_cast<int32_t *>(h->ws + h->lay.portfolios);
+  return ASTRA_OK;
+}
+
+int astra_market_shape(const astra_market *h, int32_t *M, int32_t *L, int32_t *O, int32_t *F,
+                       int32_t *C) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "astra_market_shape: null handle");
+  if (M) *M = h->M;
+  if (L) *L = h->L;
+  if (O) *O = h->O;
+  if (F) *F = h->F;
+  if (C) *C = h->C;
+  return ASTRA_OK;
+}
+
+int astra_market_bbo_cache(const astra_market *h, int32_t **bbo) {
+  if (!h || !bbo) return fail(ASTRA_ERR_INVALID_ARGUMENT, "astra_market_bbo_cache: null argument");
+  *bbo = reinterpret_cast<int32_t *>(h->ws + h->lay.bbo);
   return ASTRA_OK;
 }
 

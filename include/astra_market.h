@@ -122,6 +122,18 @@ int astra_market_clear_quotes(astra_market *market, const uint8_t *reset_mask, v
  * live int32 [M, C, 2] portfolio array inside the workspace. */
 int astra_market_portfolios(const astra_market *market, int32_t **portfolios);
 
+/* The shape the market was created with (num_markets_, max_price_levels_, ...,
+ * market.h:320-330). Any pointer may be NULL. */
+int astra_market_shape(const astra_market *market, int32_t *num_markets, int32_t *max_price_levels,
+                       int32_t *max_active_orders_per_market, int32_t *max_active_fills_per_market,
+                       int32_t *num_customers);
+
+/* Device address of the BBO the last mutating call left: int32 [4, M] = best bid
+ * prices, best bid sizes, best ask prices, best ask sizes (what
+ * astra_market_get_bbos copies out; get_bbo_kernel, market.cu:280-320, computes
+ * the same values). For kernels that consume the BBO directly. */
+int astra_market_bbo_cache(const astra_market *market, int32_t **bbo);
+
 /* VecMarket::ToString (market.cu:599-691). Synchronises `stream`, formats the
  * book of market_id into buf (NUL-terminated, truncated to buflen) and stores
  * the full text length in *needed. */

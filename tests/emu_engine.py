@@ -1,6 +1,6 @@
 """The engine's own per-market code, compiled for the host, behind the same C ABI.
 
-``csrc/market.hip`` built with ``-DASTRA_HOST_EMULATION --cuda-host-only`` runs
+``csrc/*.hip`` built with ``-DASTRA_HOST_EMULATION --cuda-host-only`` runs
 every kernel body (the same __host__ __device__ functions the GPU runs) as a
 plain loop over host memory. ``EmuMarket`` drives that build through the
 prototypes of ``astra_cuda._native`` with numpy buffers standing in for device
@@ -19,18 +19,22 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 BUILD_DIR = os.path.join(HERE, "_build")
 EMU_LIB = os.path.join(BUILD_DIR, "libastra_market_emu.so")
-SRC = os.path.join(ROOT, "astra-cuda_amd", "csrc", "market.hip")
+CSRC = os.path.join(ROOT, "astra-cuda_amd", "csrc")
+SRCS = [os.path.join(CSRC, f) for f in ("market.hip", "high_low.hip")]
+DEPS = SRCS + [os.path.join(CSRC, "runtime.h"), os.path.join(ROOT, "include", "astra_market.h"),
+               os.path.join(ROOT, "include", "astra_high_low.h")]
 
 _lib = None
 
 
 def build(force: bool = False) -> str:
-    if not force and os.path.exists(EMU_LIB) and os.path.getmtime(EMU_LIB) >= os.path.getmtime(SRC):
+    if not force and os.path.exists(EMU_LIB) and \
+            os.path.getmtime(EMU_LIB) >= max(os.path.getmtime(d) for d in DEPS):
         return EMU_LIB
     os.makedirs(BUILD_DIR, exist_ok=True)
     from astra_cuda.build import hipcc
     cmd = [hipcc(), "-DASTRA_HOST_EMULATION", "--cuda-host-only", "-O2", "-g", "-std=c++17",
-           "-fPIC", "-shared", f"-I{os.path.join(ROOT, 'include')}", SRC, "-o", EMU_LIB + ".tmp"]
+           "-fPIC", "-shared", f"-I{os.path.join(ROOT, 'include')}", *SRCS, "-o", EMU_LIB + ".tmp"]
     subprocess.run(cmd, check=True, capture_output=True)
     os.replace(EMU_LIB + ".tmp", EMU_LIB)
     return EMU_LIB
@@ -197,3 +201,70 @@ class EmuAdapter:
 
     def to_string(self, m):
         return self.mk.to_string(m)
+
+
+class EmuHighLow:
+    """The high-low game's move kernels (csrc/high_low.hip) on the emulation build,
+    with numpy arrays as the state tensors (high_low_trading.h:85-115). The setup
+    arrays (contract values, settle flags, permutation, targets) are set directly."""
+
+    def __init__(self, N, P, T, S, cM, V, market_shape):
+        from astra_cuda._native import HLObservation, HLTrade
+        self.N, self.P, self.T, self.S, self.cM, self.V = N, P, T, S, cM, V
+        L, O, F, C = market_shape
+        self.market = EmuMarket(N, L, O, F, C)
+        self.fills = self.market.new_fill_batch()
+        self.bbo = self.market.new_bbo_batch()
+        z = lambda *s: np.zeros(s, np.int32)  # noqa: E731
+        self.contract_values = z(N, 3)
+        self.contract_high_settle = np.zeros(N, np.uint8)
+        self.player_permutation = z(N, P)
+        self.target_positions = z(N, P)
+        self.player_last_positions = z(N, P, 2)
+        self.player_contract_over_time = z(N, P, T, 6)
+        self.market_contract_over_time = z(N, P * T, 3)
+        self.immediate_rewards = z(N, P)
+        self.rewards_since_last_action = z(N, P)
+        self.columns = z(5, N)
+        self.errors = z(1)
+        self._HLTrade, self._HLObservation = HLTrade, HLObservation
+
+    def trade(self, move, player, tmn, check=1):
+        self.move = np.ascontiguousarray(move, np.int32)
+        t = self._HLTrade()
+        ptr = lambda a: a.ctypes.data  # noqa: E731
+        for name in ("columns", "player_last_positions", "target_positions", "contract_values",
+                     "player_contract_over_time", "market_contract_over_time", "immediate_rewards",
+                     "rewards_since_last_action", "errors"):
+            setattr(t, name, ptr(getattr(self, name)))
+        t.move = ptr(self.move)
+        for f in EmuFills.FIELDS:
+            setattr(t, f, ptr(getattr(self.fills, f)))
+        for f in EmuBBO.FIELDS:
+            setattr(t, f, ptr(getattr(self.bbo, f)))
+        t.players, t.steps_per_player = self.P, self.T
+        t.max_contracts_per_trade, t.max_contract_value = self.S, self.V
+        t.player, t.trade_move_number, t.check = player, tmn, check
+        return lib().astra_high_low_trade(self.market.h, ctypes.byref(t), None)
+
+    def observation(self, player, current_round):
+        import math
+        v = np.zeros((self.N, 6 + 1 + 6 * self.P + 5), np.float32)
+        o = self._HLObservation()
+        ptr = lambda a: a.ctypes.data  # noqa: E731
+        o.values = ptr(v)
+        o.player_permutation = ptr(self.player_permutation)
+        o.contract_values = ptr(self.contract_values)
+        o.contract_high_settle = ptr(self.contract_high_settle)
+        o.target_positions = ptr(self.target_positions)
+        o.player_contract_over_time = ptr(self.player_contract_over_time)
+        o.best_bid_prices, o.best_ask_prices = ptr(self.bbo.best_bid_prices), ptr(self.bbo.best_ask_prices)
+        o.best_bid_sizes, o.best_ask_sizes = ptr(self.bbo.best_bid_sizes), ptr(self.bbo.best_ask_sizes)
+        o.last_prices = ptr(self.bbo.last_prices)
+        o.num_envs, o.players, o.steps_per_player = self.N, self.P, self.T
+        o.player, o.current_round = player, current_round
+        angle = 2.0 * math.pi * player / self.P
+        o.player_sin, o.player_cos = float(np.float32(math.sin(angle))), float(np.float32(math.cos(angle)))
+        o.round_fraction = float(np.float32(current_round) / np.float32(self.T))
+        _check(lib().astra_high_low_observation(ctypes.byref(o), None))
+        return v

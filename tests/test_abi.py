@@ -1,5 +1,5 @@
-"""The C-ABI library loads, exports what include/astra_market.h declares, and
-validates shapes like the reference constructor (CPU only: no device calls)."""
+"""The C-ABI library loads, exports what include/*.h declares, and validates
+shapes like the reference constructor (CPU only: no device calls)."""
 import ctypes
 import os
 import re
@@ -7,7 +7,8 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "astra_market.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
 
 
 def _ensure_built():
@@ -18,16 +19,20 @@ def _ensure_built():
 
 
 def _declared():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(astra_\w+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(astra_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_entry_points():
     names = _declared()
     for must in ("astra_market_create", "astra_market_add_two_sided_quotes", "astra_market_get_bbos",
                  "astra_update_last_prices", "astra_market_reset", "astra_market_clear_quotes",
-                 "astra_market_clone", "astra_market_to_string", "astra_market_portfolios"):
+                 "astra_market_clone", "astra_market_to_string", "astra_market_portfolios",
+                 "astra_market_shape", "astra_market_bbo_cache", "astra_high_low_trade",
+                 "astra_high_low_observation"):
         assert must in names
 
 

@@ -1,0 +1,133 @@
+"""The high-low trading game on the HIP engine (astra_cuda.load_game) against the
+game oracle, bit-exact (GPU)."""
+import numpy as np
+import pytest
+import torch
+
+from high_low_cases import HAND_GAME, random_game
+from oracle.high_low_oracle import MAX_CHANCE_NODES, OracleHighLow
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _t(a):
+    return torch.as_tensor(np.ascontiguousarray(a)).to(DEV)
+
+
+def _game(params):
+    import astra_cuda as astra
+    astra.register_games()
+    return astra.load_game("high_low_trading", params)
+
+
+def _compare(o, s, where):
+    for name in ("player_last_positions", "player_contract_over_time", "market_contract_over_time",
+                 "immediate_rewards", "rewards_since_last_action", "target_positions", "contract_values"):
+        assert np.array_equal(getattr(o, name), getattr(s, name).cpu().numpy()), (where, name)
+    P = o.P
+    assert np.array_equal(o.market.customer_portfolios, s.market.get_customer_portfolios().cpu().numpy()), where
+    for f in ("best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes", "last_prices"):
+        assert np.array_equal(getattr(o.bbo, f), getattr(s.bbo_batch, f).cpu().numpy()), (where, f)
+    rb = torch.zeros((o.N, P), dtype=torch.float32, device=DEV)
+    s.fill_rewards(rb)
+    assert np.array_equal(o.fill_rewards(), rb.cpu().numpy()), where
+    one = torch.zeros((o.N,), dtype=torch.float32, device=DEV)
+    for p in range(P):
+        s.fill_rewards_since_last_action(one, p)
+        assert np.array_equal(o.fill_rewards_since_last_action(p), one.cpu().numpy()), (where, p)
+
+
+def _params(N, P, T, S, cM, V, shape):
+    p = dict(num_markets=N, players=P, steps_per_player=T, max_contracts_per_trade=S,
+             customer_max_size=cM, max_contract_value=V)
+    if shape is not None:
+        p.update(market_price_levels=shape[0], market_orders=shape[1], market_fills=shape[2],
+                 market_customers=shape[3])
+    return p
+
+
+@pytest.mark.parametrize("N,P,T,S,cM,V,shape,seed", [
+    (500, 5, 4, 5, 5, 30, None, 1),
+    (300, 4, 6, 3, 4, 20, (21, 12, 6, 4), 2),         # ring of 12: slot reuse
+    (2000, 5, 3, 5, 5, 127, (128, 1024, 10, 16), 3),  # the config-5 shape
+])
+def test_gpu_game_vs_oracle(N, P, T, S, cM, V, shape, seed):
+    print(f"game N={N} P={P} T={T} shape={shape}", flush=True)
+    rng = np.random.default_rng(seed)
+    o = OracleHighLow(N, P, T, S, cM, V, market_shape=shape)
+    g = _game(_params(N, P, T, S, cM, V, shape))
+    s = g.new_initial_state()
+    chance, moves = random_game(rng, N, P, T, S, cM, V)
+    for c in chance:
+        assert s.is_chance_node() and s.current_player() == -1
+        o.apply_action(c)
+        s.apply_action(_t(c))
+    values = torch.zeros(g.observation_tensor_shape(), dtype=torch.float32, device=DEV)
+    for k, mv in enumerate(moves):
+        assert s.current_player() == o.current_player() == k % P
+        if k % 2 == 0:  # the rollout loop's observation of the acting player
+            assert s.fill_observation_tensor(values) == k % P
+            assert np.array_equal(o.fill_observation_tensor(k % P), values.cpu().numpy()), k
+        o.apply_action(mv)
+        assert s.apply_action(_t(mv)) == k % P
+        _compare(o, s, f"move {k}")
+        if k == len(moves) // 2:  # a clone continues identically
+            s2, o2 = s.clone(), o  # o keeps going; compare the clone at the end
+            clone_at = k
+    assert s.is_terminal() and o.is_terminal()
+    ret = torch.zeros((N, P), dtype=torch.float32, device=DEV)
+    s.fill_returns(ret)
+    assert np.array_equal(o.fill_returns(), ret.cpu().numpy())
+    info = s.expose_info()
+    assert np.array_equal(info["players"].cpu().numpy(), o.player_contract_over_time)
+    assert np.array_equal(info["market"].cpu().numpy(), o.market_contract_over_time)
+    for mv in moves[clone_at + 1:]:
+        s2.apply_action(_t(mv))
+    _compare(o, s2, "clone")
+    s.reset()
+    assert s.move_number() == 0 and not s.player_contract_over_time.any()
+    assert not s.market.get_customer_portfolios().any()
+
+
+def test_gpu_hand_game():
+    g = _game(HAND_GAME["params"])
+    s = g.new_initial_state()
+    for c in HAND_GAME["chance"]:
+        s.apply_action(_t(c))
+    values = torch.zeros(g.observation_tensor_shape(), dtype=torch.float32, device=DEV)
+    for k, mv in enumerate(HAND_GAME["moves"]):
+        s.apply_action(_t(np.array([mv], np.int32)))
+        assert s.immediate_rewards[0].tolist() == HAND_GAME["immediate"][k]
+        assert s.rewards_since_last_action[0].tolist() == HAND_GAME["since_last"][k]
+        assert s.market_contract_over_time[0, k].tolist() == HAND_GAME["market_rows"][k]
+        if k in HAND_GAME["portfolios_after"]:
+            assert s.market.get_customer_portfolios()[0].tolist() == HAND_GAME["portfolios_after"][k]
+        if k == HAND_GAME["obs_after"]:
+            s.fill_observation_tensor(HAND_GAME["obs_player"], values)
+            assert values[0].tolist() == HAND_GAME["obs"]
+    ret = torch.zeros((1, 4), dtype=torch.float32, device=DEV)
+    s.fill_returns(ret)
+    assert ret[0].tolist() == HAND_GAME["returns"]
+
+
+def test_gpu_move_checks():
+    prm = dict(HAND_GAME["params"], num_markets=5)
+    s = _game(prm).new_initial_state()
+    for c in HAND_GAME["chance"]:
+        s.apply_action(_t(np.repeat(c, 5, axis=0)))
+    bad = np.tile(np.array([[12, 18, 2, 1]], np.int32), (5, 1))
+    bad[3, 3] = 6  # ask size above max_contracts_per_trade
+    with pytest.raises(RuntimeError, match="Astra Fatal Error.*ask_sizes"):
+        s.apply_action(_t(bad))
+    assert s.move_number() == MAX_CHANCE_NODES and s.market.global_tid == 0
+    s.apply_action(_t(np.tile(np.array([[12, 18, 2, 1]], np.int32), (5, 1))))  # good move goes through
+    assert s.move_number() == MAX_CHANCE_NODES + 1
+    # unchecked: no sync per move; check_errors reports afterwards
+    s2 = _game(dict(prm, check_moves=False)).new_initial_state()
+    for c in HAND_GAME["chance"]:
+        s2.apply_action(_t(np.repeat(c, 5, axis=0)))
+    s2.apply_action(_t(bad))
+    with pytest.raises(RuntimeError, match="ask_sizes <= max_contracts_per_trade"):
+        s2.check_errors()
+    s2.check_errors()  # cleared

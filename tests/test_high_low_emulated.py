@@ -1,0 +1,93 @@
+"""The high-low game's move kernels (csrc/high_low.hip), compiled for the host,
+against the game oracle (CPU only). The chance-move set-up is copied from the
+oracle; every trading move then runs through astra_high_low_trade and every
+state array is compared; observations through astra_high_low_observation."""
+import numpy as np
+import pytest
+
+from emu_engine import EmuHighLow
+from high_low_cases import HAND_GAME, random_game
+from oracle.high_low_oracle import MAX_CHANCE_NODES, OracleHighLow
+
+STATE = ("player_last_positions", "player_contract_over_time", "market_contract_over_time",
+         "immediate_rewards", "rewards_since_last_action")
+
+
+def _setup(o, e):
+    e.contract_values[:] = o.contract_values
+    e.contract_high_settle[:] = o.contract_high_settle
+    e.player_permutation[:] = o.player_permutation
+    e.target_positions[:] = o.target_positions
+
+
+def _compare(o, e, where):
+    for name in STATE:
+        assert np.array_equal(getattr(o, name), getattr(e, name)), (where, name)
+    assert np.array_equal(o.market.customer_portfolios, e.market.portfolios), where
+    for f in ("best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes", "last_prices"):
+        assert np.array_equal(getattr(o.bbo, f), getattr(e.bbo, f)), (where, f)
+    assert np.array_equal(o.fills.fill_counts, e.fills.fill_counts), where
+
+
+def _play(N, P, T, S, cM, V, shape, seed, obs_every=3):
+    rng = np.random.default_rng(seed)
+    o = OracleHighLow(N, P, T, S, cM, V, market_shape=shape)
+    e = EmuHighLow(N, P, T, S, cM, V, (o.L, o.O, o.F, o.C))
+    chance, moves = random_game(rng, N, P, T, S, cM, V)
+    for c in chance:
+        o.apply_action(c)
+    _setup(o, e)
+    for k, mv in enumerate(moves):
+        player = o.current_player()
+        o.apply_action(mv)
+        assert e.trade(mv, player, k) == 0
+        _compare(o, e, f"move {k}")
+        if k % obs_every == 0 and k + 1 < T * P:
+            cr = (o.move_number - MAX_CHANCE_NODES) // P
+            for p in range(P):
+                assert np.array_equal(o.fill_observation_tensor(p), e.observation(p, cr)), (k, p)
+
+
+@pytest.mark.parametrize("N,P,T,S,cM,V,shape,seed", [
+    (37, 4, 3, 5, 5, 30, None, 1),          # the game's own market shape
+    (64, 5, 6, 5, 5, 30, None, 2),
+    (50, 5, 8, 3, 4, 20, (21, 12, 6, 5), 3),  # a ring of 12 wraps: slot reuse
+    (40, 6, 4, 5, 5, 127, (128, 1024, 10, 16), 4),  # the config-5 shape (C > players)
+])
+def test_emulated_game_vs_oracle(N, P, T, S, cM, V, shape, seed):
+    _play(N, P, T, S, cM, V, shape, seed)
+
+
+def test_emulated_hand_game():
+    prm = HAND_GAME["params"]
+    o = OracleHighLow(**prm)
+    e = EmuHighLow(1, prm["players"], prm["steps_per_player"], prm["max_contracts_per_trade"],
+                   prm["customer_max_size"], prm["max_contract_value"], (o.L, o.O, o.F, o.C))
+    for c in HAND_GAME["chance"]:
+        o.apply_action(c)
+    _setup(o, e)
+    for k, mv in enumerate(HAND_GAME["moves"]):
+        player = o.current_player()
+        o.apply_action(np.array([mv], np.int32))
+        assert e.trade(np.array([mv], np.int32), player, k) == 0
+        assert e.immediate_rewards[0].tolist() == HAND_GAME["immediate"][k]
+        assert e.rewards_since_last_action[0].tolist() == HAND_GAME["since_last"][k]
+        assert e.market_contract_over_time[0, k].tolist() == HAND_GAME["market_rows"][k]
+        if k == HAND_GAME["obs_after"]:
+            assert e.observation(HAND_GAME["obs_player"], 1)[0].tolist() == HAND_GAME["obs"]
+
+
+def test_emulated_checks_flag_and_stop():
+    N, P, T, S, cM, V = 6, 4, 2, 5, 5, 30
+    o = OracleHighLow(N, P, T, S, cM, V)
+    e = EmuHighLow(N, P, T, S, cM, V, (o.L, o.O, o.F, o.C))
+    mv = np.tile(np.array([[12, 18, 2, 1]], np.int32), (N, 1))
+    mv[2, 2] = S + 1     # bid size above max_contracts_per_trade
+    mv[4, 0] = 0         # bid price not > 0
+    rc = e.trade(mv, 0, 0, check=1)
+    assert rc != 0
+    assert e.errors[0] == (1 << 0) | (1 << 6)
+    assert e.market.global_tid == 0 and not e.fills.fill_counts.any()  # nothing traded
+    e.errors[0] = 0
+    assert e.trade(mv, 0, 0, check=0) == 0  # no check: trades, flag kept for the caller
+    assert e.errors[0] == (1 << 0) | (1 << 6) and e.market.global_tid == 2

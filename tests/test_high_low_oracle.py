@@ -1,0 +1,74 @@
+"""The high-low game oracle (oracle/high_low_oracle.py) against hand-derived values
+and identities of the reward formula (CPU only)."""
+import numpy as np
+import pytest
+
+from high_low_cases import HAND_GAME, random_game
+from oracle.high_low_oracle import GameError, OracleHighLow
+
+
+def _play_hand(o):
+    for c in HAND_GAME["chance"]:
+        o.apply_action(c)
+    out = []
+    for k, mv in enumerate(HAND_GAME["moves"]):
+        o.apply_action(np.array([mv], np.int32))
+        out.append((o.immediate_rewards[0].tolist(), o.rewards_since_last_action[0].tolist(),
+                    o.market.customer_portfolios[0].tolist(), o.market_contract_over_time[0, k].tolist()))
+        if k == HAND_GAME["obs_after"]:
+            obs = o.fill_observation_tensor(HAND_GAME["obs_player"])[0].tolist()
+    return out, obs
+
+
+def test_oracle_hand_game():
+    o = OracleHighLow(**{k: v for k, v in HAND_GAME["params"].items()})
+    assert (o.L, o.O, o.F, o.C) == (31, 16, 10, 4)  # high_low_trading.cc:57-69
+    out, obs = _play_hand(o)
+    for k, (imm, since, pf, mrow) in enumerate(out):
+        assert imm == HAND_GAME["immediate"][k], k
+        assert since == HAND_GAME["since_last"][k], k
+        assert mrow == HAND_GAME["market_rows"][k], k
+        if k in HAND_GAME["portfolios_after"]:
+            assert pf == HAND_GAME["portfolios_after"][k], k
+    assert o.is_terminal() and o.current_player() == -4
+    assert o.fill_returns()[0].tolist() == HAND_GAME["returns"]
+    assert obs == pytest.approx(HAND_GAME["obs"], abs=0, rel=0)
+    info = o.expose_info()
+    assert info["players"][0, 3, 0].tolist() == [26, 24, 2, 1, 1, -25]
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_reward_telescopes_to_returns(seed):
+    """Without penalties (no crossing quote of one's own, no zero size), each player's
+    immediate rewards over a game sum to FillReturns + |target| * V for a customer:
+    the position term telescopes from |0 - target| and the cash term from 0, and the
+    last move adds the settlement (high_low_trading.cc:290-328 against :344-373)."""
+    rng = np.random.default_rng(seed)
+    N, P, T, S, cM, V = 40, 5, 4, 5, 5, 30
+    o = OracleHighLow(N, P, T, S, cM, V)
+    chance, _ = random_game(rng, N, P, T, S, cM, V)
+    for c in chance:
+        o.apply_action(c)
+    total = np.zeros((N, P), np.int64)
+    for _ in range(T * P):
+        bid = rng.integers(1, V, N)
+        ask = np.minimum(bid + rng.integers(1, 4, N), V)
+        bid = np.minimum(bid, ask - 1)
+        mv = np.stack([bid, ask, rng.integers(1, S + 1, N), rng.integers(1, S + 1, N)], 1).astype(np.int32)
+        o.apply_action(mv)
+        total += o.immediate_rewards
+    ret = o.fill_returns().astype(np.int64)
+    bonus = (o.target_positions != 0) * np.abs(o.target_positions) * V
+    assert np.array_equal(total, ret + bonus)
+    # and the cash moved by the market sums to zero across players in every env
+    assert not o.market.customer_portfolios[:, :, 1].astype(np.int64).sum(axis=1).any()
+
+
+def test_input_checks_stop_before_trading():
+    o = OracleHighLow(3, 4, 2, 5, 5, 30)
+    for c in HAND_GAME["chance"]:
+        o.apply_action(np.repeat(c, 3, axis=0))
+    bad = np.array([[12, 18, 2, 1], [12, 31, 2, 1], [12, 18, 2, 1]], np.int32)  # ask price > V
+    with pytest.raises(GameError, match="ask_prices <= max_contract_value"):
+        o.apply_action(bad)
+    assert o.move_number == 4 and o.market.global_tid == 0
