@@ -318,6 +318,10 @@ class HighLowTradingState:
             self._errors.zero_()
             _fatal(_native.last_error())
 
+    def set_check_moves(self, check: bool) -> None:
+        """Switch the per-move input checks (one sync per move) on or off."""
+        self._trade.check = 1 if check else 0
+
     def check_errors(self) -> None:
         """With check_moves=False: raise if any move since the last call failed the
         reference's input checks (high_low_trading.cc:264-271). Synchronises."""

@@ -170,3 +170,65 @@ class QuoteStream:
             for arr, v in zip(out, self.step(t)):
                 arr[i] = v
         return tuple(out)
+
+
+# ---- config 5: the high-low trading game step ----
+F_GAME_CAND, F_GAME_HL, F_GAME_PERM, F_GAME_CUST, F_GAME_MOVE = 64, 66, 67, 80, 96  # 80+j, 96+c
+
+
+@dataclass(frozen=True)
+class GameConfig:
+    """Config 5: 10,000 envs of the high-low game, 5 players, 200 steps per player
+    (1,000 trading moves), on a market of 128 levels, 1,024 orders and 16 customers
+    (the shape BASELINE names; the game's own sizing would be smaller). Prices are
+    U[1, max_contract_value], sizes U[0, max_contracts_per_trade]: a random policy
+    over the legal actions."""
+    index: int = 5
+    name: str = "game_step_10k"
+    envs: int = 10_000
+    players: int = 5
+    steps_per_player: int = 200
+    max_contracts_per_trade: int = 5
+    customer_max_size: int = 5
+    max_contract_value: int = 127
+    market_shape: tuple = (128, 1024, 10, 16)
+
+    def game_params(self, envs: int | None = None, check_moves: bool = True) -> dict:
+        L, O, F, C = self.market_shape
+        return dict(num_markets=envs or self.envs, players=self.players,
+                    steps_per_player=self.steps_per_player,
+                    max_contracts_per_trade=self.max_contracts_per_trade,
+                    customer_max_size=self.customer_max_size,
+                    max_contract_value=self.max_contract_value, market_price_levels=L,
+                    market_orders=O, market_fills=F, market_customers=C, check_moves=check_moves)
+
+
+GAME_CONFIG = GameConfig()
+
+
+class GameStream:
+    """Chance moves (as the reference's env.py:42-56 draws them) and trading moves
+    [N, 4] = (bid_px, ask_px, bid_sz, ask_sz) for envs ``envs``, from the counter
+    generator."""
+
+    def __init__(self, cfg: GameConfig = GAME_CONFIG, envs: np.ndarray | None = None, seed: int = 0):
+        self.cfg, self.seed = cfg, seed
+        self.envs = np.arange(cfg.envs, dtype=np.int64) if envs is None else np.asarray(envs, np.int64)
+
+    def chance(self):
+        c, s, e = self.cfg, self.seed, self.envs
+        V, P, cM = c.max_contract_value, c.players, c.customer_max_size
+        cand = np.stack([uniform(s, F_GAME_CAND + j, 0, e, 1, V) for j in range(2)], 1)
+        hl = uniform(s, F_GAME_HL, 0, e, 0, 1)
+        keys = np.stack([draws(s, F_GAME_PERM, j, e) for j in range(P)], 1)
+        perm = np.argsort(keys, axis=1, kind="stable").astype(np.int32)
+        cs = np.stack([uniform(s, F_GAME_CUST + j, 0, e, -cM, cM - 1) for j in range(P - 3)], 1)
+        cs[cs >= 0] += 1
+        return [cand.astype(np.int32), hl.astype(np.int32), perm, cs.astype(np.int32)]
+
+    def move(self, k: int):
+        c, s, e = self.cfg, self.seed, self.envs
+        V, S = c.max_contract_value, c.max_contracts_per_trade
+        return np.stack([uniform(s, F_GAME_MOVE + 0, k, e, 1, V), uniform(s, F_GAME_MOVE + 1, k, e, 1, V),
+                         uniform(s, F_GAME_MOVE + 2, k, e, 0, S), uniform(s, F_GAME_MOVE + 3, k, e, 0, S)],
+                        1).astype(np.int32)

@@ -48,7 +48,8 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=900, help="timed steps K")
     ap.add_argument("--warmup", type=int, default=100, help="untimed warm-up steps W")
-    ap.add_argument("--config", type=int, default=3, help="BASELINE.json config index (2, 3 or 4)")
+    ap.add_argument("--config", type=int, default=3,
+                    help="BASELINE.json config index (2, 3 or 4; 5 = the high-low game step)")
     ap.add_argument("--markets", type=int, default=0, help="override the config's market count")
     ap.add_argument("--no-bbo", action="store_true", help="do not call get_bbos every step")
     ap.add_argument("--latency-steps", type=int, default=300)
@@ -99,6 +100,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         return copy_calibration()
+
+    if args.config == 5:
+        return bench_game(args)
 
     import numpy as np
     import torch
@@ -249,6 +253,166 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, cfg, host, M, W, K, bbo)
     print(json.dumps(result), flush=True)
+
+
+def bench_game(args):
+    """Config 5: one trading move of every env of the high-low game per step
+    (HighLowTradingState::ApplyPlayerTrading: AddTwoSidedQuotes, GetBBOs,
+    UpdateLastPrices and the per-player rewards and telemetry). The chance moves
+    are applied before timing; the timed steps are trading moves W..W+K-1 of one
+    game (W + K <= players * steps_per_player)."""
+    import numpy as np
+    import torch
+    import astra_cuda as astra
+    from astra_cuda.workloads import GAME_CONFIG, GameStream
+
+    cfg = GAME_CONFIG
+    N = args.markets or cfg.envs
+    P = cfg.players
+    moves_total = P * cfg.steps_per_player
+    W, K = args.warmup, args.steps
+    if W + K > moves_total:
+        print(f"config 5 has {moves_total} trading moves: warmup + steps must not exceed it",
+              file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    t0 = time.perf_counter()
+    gs = GameStream(cfg, np.arange(N))
+    chance = gs.chance()
+    host_moves = [gs.move(k) for k in range(W + K)]
+    moves = [torch.from_numpy(m).to(dev) for m in host_moves]
+    chance_d = [torch.from_numpy(c).to(dev) for c in chance]
+    torch.cuda.synchronize()
+    log(f"generated config 5 moves: {W + K} moves x {N} envs in {time.perf_counter() - t0:.1f}s")
+    astra.register_games()
+    game = astra.load_game("high_low_trading", cfg.game_params(N, check_moves=True))
+    state = game.new_initial_state()
+    for c in chance_d:
+        state.apply_action(c)
+    for k in range(W):
+        state.apply_action(moves[k])
+    torch.cuda.synchronize()
+    snaps = [state.clone() for _ in range(4)]
+    torch.cuda.synchronize()
+    log(f"warm-up done ({W} moves); timing {K} moves")
+
+    def timed(st, check):
+        st.set_check_moves(check)
+        torch.cuda.synchronize()
+        a0 = time.perf_counter()
+        for k in range(W, W + K):
+            st.apply_action(moves[k])
+        torch.cuda.synchronize()
+        return time.perf_counter() - a0
+
+    wall = timed(state, True)                 # A: with the reference's input checks
+    wall_unchecked = timed(snaps[0], False)   # A': checks deferred (no sync per move)
+    log(f"A: {K} moves in {wall * 1e3:.2f} ms (checked), {wall_unchecked * 1e3:.2f} ms (unchecked)")
+    # B: per-move latency, checked
+    st = snaps[1]
+    lat = []
+    for k in range(W, W + min(K, args.latency_steps)):
+        torch.cuda.synchronize()
+        h0 = time.perf_counter()
+        st.apply_action(moves[k])
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - h0)
+    lat_ms = np.array(lat) * 1e3
+    # C: device time per move (three kernels), unchecked moves back to back
+    st = snaps[2]
+    st.set_check_moves(False)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for k in range(W, W + K):
+        st.apply_action(moves[k])
+    ev[1].record()
+    torch.cuda.synchronize()
+    step_ms = ev[0].elapsed_time(ev[1]) / K
+    # D: work counts of the matching kernel
+    st = snaps[3]
+    st.set_check_moves(False)
+    counters = torch.zeros(8, dtype=torch.int64, device=dev)
+    st.market._set_stats(counters)
+    for k in range(W, W + K):
+        st.apply_action(moves[k])
+    torch.cuda.synchronize()
+    st.market._set_stats(None)
+    n_ins, n_fill, n_empty = (int(x) for x in counters.cpu().tolist()[:3])
+    # algorithmic bytes per move: the matching kernel's (24 B per env + 32 per insert +
+    # 109 per fill row + 8 per emptied level) plus the move kernels': move 16 B, input
+    # columns 20 B and a 16*P B portfolio snapshot before; BBO 32 B, fill count and
+    # last price 8 B, move 16 B, telemetry 28 + 8*P B, and per player portfolio and
+    # snapshot 16 B, target 4 B, rewards 12 B after, plus the contract value 4 B.
+    game_bytes = N * ((16 + 20 + 16 * P) + (32 + 8 + 16 + 28 + 8 * P + 4 + 32 * P))
+    step_bytes = (24.0 * N * K + 32.0 * n_ins + 109.0 * n_fill + 8.0 * n_empty) / K + game_bytes
+    achieved = step_bytes / (step_ms * 1e-3) / 1e9
+    result = {
+        "metric": "quote-matches/sec and market-steps/sec at 100k markets; p50 step latency",
+        "value": N * K / wall,
+        "unit": "quote-matches/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": wall / K * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"config5_{cfg.name}", "envs": N, "players": P,
+            "steps_per_player": cfg.steps_per_player, "max_contract_value": cfg.max_contract_value,
+            "max_contracts_per_trade": cfg.max_contracts_per_trade,
+            "market_shape_LOFC": list(cfg.market_shape), "move_checks": "one sync per move",
+            "parallelism": "single GPU, one lane per env",
+        },
+        "market_steps_per_s": K / wall,
+        "value_unchecked": N * K / wall_unchecked,
+        "ms_per_step_unchecked": wall_unchecked / K * 1e3,
+        "p50_step_latency_ms": float(np.percentile(lat_ms, 50)),
+        "p99_step_latency_ms": float(np.percentile(lat_ms, 99)),
+        "device_ms_per_step": {"move_kernels": step_ms},
+        "work_per_step": {"inserts": n_ins / K, "fill_rows": n_fill / K, "levels_emptied": n_empty / K},
+        "roofline": {
+            "kernel": "trade_pre + quote_match + trade_post", "bound": "hbm",
+            "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None, "algorithmic_bytes_per_launch": step_bytes,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = game_cpu_baseline(args, cfg, chance, host_moves, N, W, K)
+    print(json.dumps(result), flush=True)
+
+
+def game_cpu_baseline(args, cfg, chance, host_moves, N, W, K):
+    """The game oracle (numpy state operations over the C market oracle, one
+    thread) on the first envs of the same stream."""
+    import numpy as np
+    from oracle.high_low_oracle import OracleHighLow
+
+    model, avail = cpu_info()
+
+    def run(n, steps):
+        o = OracleHighLow(n, cfg.players, cfg.steps_per_player, cfg.max_contracts_per_trade,
+                          cfg.customer_max_size, cfg.max_contract_value, market_shape=cfg.market_shape)
+        for c in chance:
+            o.apply_action(np.ascontiguousarray(c[:n]))
+        for k in range(W):
+            o.apply_action(np.ascontiguousarray(host_moves[k][:n]))
+        c0 = time.perf_counter()
+        for k in range(W, W + steps):
+            o.apply_action(np.ascontiguousarray(host_moves[k][:n]))
+        return n * steps / (time.perf_counter() - c0)
+
+    rate = run(min(N, 1000), min(K, 50))
+    n = int(min(N, max(500, rate * args.cpu_seconds / K)))
+    log(f"CPU leg: {n} envs x {K} moves")
+    v = run(n, K)
+    return {"value": v, "unit": "quote-matches/s", "cores": 1, "kind": "port",
+            "sample": f"envs 0..{n - 1} of the same config-5 stream, the same {W} warm-up + {K} timed moves",
+            "host_cpu": model, "host_cpus_available": avail}
 
 
 def measured_traffic(cfg, M, bbo):
