@@ -29,6 +29,8 @@ PROTOTYPES = {
     "astra_market_add_two_sided_quotes": (_c_int, [_vp] + [_vp] * 5 + [_vp] * 9 + [_vp]),
     "astra_market_get_bbos": (_c_int, [_vp] + [_vp] * 4 + [_vp]),
     "astra_update_last_prices": (_c_int, [_vp, _vp, _vp, _c_i32, _c_i32, _vp]),
+    "astra_market_add_two_sided_quotes_rows": (_c_int, [_vp] + [_vp] * 5 + [_vp, _vp, _vp]),
+    "astra_update_last_prices_rows": (_c_int, [_vp, _vp, _vp, _c_i32, _c_i32, _vp]),
     "astra_fill_i32": (_c_int, [_vp, ctypes.c_int64, _c_i32, _vp]),
     "astra_market_reset": (_c_int, [_vp, _vp]),
     "astra_market_clear_quotes": (_c_int, [_vp, _vp, _vp]),
@@ -53,7 +55,7 @@ class HLTrade(ctypes.Structure):
         "rewards_since_last_action", "fill_prices", "fill_sizes", "fill_customer_ids",
         "fill_quoter_ids", "fill_is_sell_quote", "fill_quote_sizes", "fill_tid", "fill_quote_tid",
         "fill_counts", "best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes",
-        "last_prices", "errors")] + [(n, _c_i32) for n in (
+        "last_prices", "fill_rows", "errors")] + [(n, _c_i32) for n in (
         "players", "steps_per_player", "max_contracts_per_trade", "max_contract_value", "player",
         "trade_move_number", "check")]
 

@@ -140,7 +140,9 @@ class HighLowTradingState:
             self.immediate_rewards = torch.zeros((N, P), **i32)
             self.rewards_since_last_action = torch.zeros((N, P), **i32)
             self.bbo_batch = self.market.new_bbo_batch()
-            self.fill_batch = self.market.new_fill_batch()
+            # the fills stay inside the state, so the row layout (one 32-byte write
+            # per fill) costs callers nothing
+            self.fill_batch = self.market.new_fill_batch(layout="rows")
             self._move_number = 0
         else:  # copy constructor (high_low_trading.cc:104-123)
             o = _clone_of
@@ -171,9 +173,13 @@ class HighLowTradingState:
             "rewards_since_last_action": self.rewards_since_last_action,
             "errors": self._errors,
         }
-        for f in ("fill_prices", "fill_sizes", "fill_customer_ids", "fill_quoter_ids", "fill_is_sell_quote",
-                  "fill_quote_sizes", "fill_tid", "fill_quote_tid", "fill_counts"):
-            ptrs[f] = getattr(fb, f)
+        ptrs["fill_counts"] = fb.fill_counts
+        if fb._rows is not None:
+            ptrs["fill_rows"] = fb._rows
+        else:
+            for f in ("fill_prices", "fill_sizes", "fill_customer_ids", "fill_quoter_ids", "fill_is_sell_quote",
+                      "fill_quote_sizes", "fill_tid", "fill_quote_tid"):
+                ptrs[f] = getattr(fb, f)
         for f in ("best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes", "last_prices"):
             ptrs[f] = getattr(bb, f)
         for k, v in ptrs.items():

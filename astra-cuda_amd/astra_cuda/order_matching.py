@@ -72,28 +72,64 @@ class FillBatch:
     ``[M, F]``; ``fill_is_sell_quote``: bool ``[M, F]``; ``fill_counts``: int32
     ``[M]`` (``-1`` marks a market that ran out of fill slots). Only
     ``[m, :fill_counts[m]]`` is written by a call; later entries keep older values.
+
+    Layout: by default (``"columns"``) each field is its own contiguous tensor, as in
+    the reference. ``VecMarket.new_fill_batch(layout="rows")`` keeps the eight
+    per-row fields side by side in one int32 ``[M, F, 8]`` buffer and exposes them
+    as strided ``[M, F]`` views with the same values (a row is then one 32-byte
+    write for the engine); assigning a field replaces the layout by "columns".
     """
 
     FIELDS = ("fill_prices", "fill_sizes", "fill_customer_ids", "fill_quoter_ids",
               "fill_is_sell_quote", "fill_quote_sizes", "fill_tid", "fill_quote_tid",
               "fill_counts")
-    __slots__ = FIELDS + ("_pack",)
+    __slots__ = FIELDS + ("_pack", "_rows")
 
     def __init__(self):
         for f in self.FIELDS:
             object.__setattr__(self, f, None)
         object.__setattr__(self, "_pack", None)
+        object.__setattr__(self, "_rows", None)
 
     def __setattr__(self, name, value):
         object.__setattr__(self, name, value)
         if name in FillBatch.FIELDS:
             object.__setattr__(self, "_pack", None)
+            if name != "fill_counts":
+                object.__setattr__(self, "_rows", None)
+
+    def _set_rows(self, rows: torch.Tensor, counts: torch.Tensor) -> None:
+        """Point the eight row fields at views of ``rows`` (int32 [M, F, 8])."""
+        for i, f in enumerate(self.FIELDS[:8]):
+            v = rows.view(torch.uint8)[:, :, 16].view(torch.bool) if f == "fill_is_sell_quote" else rows[:, :, i]
+            object.__setattr__(self, f, v)
+        object.__setattr__(self, "fill_counts", counts)
+        object.__setattr__(self, "_rows", rows)
+        object.__setattr__(self, "_pack", None)
+
+    @property
+    def layout(self) -> str:
+        return "rows" if self._rows is not None else "columns"
 
     def _pointers(self, M: int, F: int, device: torch.device):
-        """Validated device pointers of the 9 fields (cached until a field is reassigned)."""
+        """Validated device pointers (cached until a field is reassigned): the nine
+        fields, or ("rows", rows, fill_counts) for the row layout."""
         pack = self._pack
         if pack is not None and pack[0] == (M, F, device):
             return pack[1]
+        rows = self._rows
+        if rows is not None:
+            fc = self.fill_counts
+            if tuple(rows.shape) != (M, F, 8) or rows.dtype != torch.int32 or not rows.is_contiguous():
+                _fatal(f"fills row buffer must be int32 [{M}, {F}, 8]")
+            if not isinstance(fc, torch.Tensor) or tuple(fc.shape) != (M,) or fc.dtype != torch.int32 \
+                    or not fc.is_contiguous():
+                _fatal(f"fills.fill_counts must be a contiguous int32 tensor of shape [{M}]")
+            if rows.device != device or fc.device != device:
+                _fatal(f"fills tensors must be on device {device.index}")
+            ptrs = ("rows", rows.data_ptr(), fc.data_ptr())
+            object.__setattr__(self, "_pack", ((M, F, device), ptrs))
+            return ptrs
         ptrs = []
         for f in self.FIELDS:
             t = getattr(self, f)
@@ -122,8 +158,11 @@ class FillBatch:
     Reset = reset
 
     def clone(self) -> "FillBatch":
-        """Copy constructor (market.h:80-89): every tensor cloned."""
+        """Copy constructor (market.h:80-89): every tensor cloned (the layout kept)."""
         out = FillBatch()
+        if self._rows is not None:
+            out._set_rows(self._rows.clone(), self.fill_counts.clone())
+            return out
         for f in self.FIELDS:
             setattr(out, f, getattr(self, f).clone())
         return out
@@ -185,6 +224,15 @@ class BBOBatch:
     def update_last_prices(self, fills: FillBatch) -> None:
         """BBOBatch::UpdateLastPrices (market.cu:798-825): last fill price where count > 0."""
         lp, fc, fp = self.last_prices, fills.fill_counts, fills.fill_prices
+        if fills._rows is not None:
+            rows = fills._rows
+            M, F = int(rows.shape[0]), int(rows.shape[1])
+            if rows.device != lp.device or fc.device != lp.device or lp.shape[0] != M:
+                _fatal("UpdateLastPrices: fills and last_prices must match in device and markets")
+            with torch.cuda.device(lp.device):
+                _check(_native.lib().astra_update_last_prices_rows(
+                    lp.data_ptr(), fc.data_ptr(), rows.data_ptr(), M, F, _raw_stream(lp.device.index)))
+            return
         if fc.device != lp.device:  # market.cu:801-802
             _fatal(f"fills.fill_counts.device() == last_prices.device()\n"
                    f"fills.fill_counts.device() = {fc.device}, last_prices.device() = {lp.device}")
@@ -297,10 +345,18 @@ class VecMarket:
 
     # -- batches -----------------------------------------------------------
 
-    def new_fill_batch(self) -> FillBatch:
-        """NewFillBatch (market.cu:420-439): zero-initialised tensors."""
+    def new_fill_batch(self, layout: str = "columns") -> FillBatch:
+        """NewFillBatch (market.cu:420-439): zero-initialised tensors. ``layout="rows"``
+        (not in the reference) stores the eight row fields in one [M, F, 8] buffer
+        and exposes strided views of it (see FillBatch)."""
         b = FillBatch()
         M, F, dev = self._M, self._F, self._device
+        if layout == "rows":
+            b._set_rows(torch.zeros((M, F, 8), dtype=torch.int32, device=dev),
+                        torch.zeros((M,), dtype=torch.int32, device=dev))
+            return b
+        if layout != "columns":
+            _fatal(f"unknown fill batch layout {layout!r} (columns or rows)")
         for f in FillBatch.FIELDS:
             if f == "fill_counts":
                 setattr(b, f, torch.zeros((M,), dtype=torch.int32, device=dev))
@@ -343,9 +399,14 @@ class VecMarket:
             if t.dtype != torch.int32:
                 _fatal(f"{name} tensor must be int32, got {t.dtype}")
         fp = fills._pointers(M, self._F, dev)
-        rc = self._lib.astra_market_add_two_sided_quotes(
-            self._h, bid_px.data_ptr(), bid_sz.data_ptr(), ask_px.data_ptr(), ask_sz.data_ptr(),
-            customer_ids.data_ptr(), *fp, _raw_stream(self._device_index))
+        if fp[0] == "rows":
+            rc = self._lib.astra_market_add_two_sided_quotes_rows(
+                self._h, bid_px.data_ptr(), bid_sz.data_ptr(), ask_px.data_ptr(), ask_sz.data_ptr(),
+                customer_ids.data_ptr(), fp[1], fp[2], _raw_stream(self._device_index))
+        else:
+            rc = self._lib.astra_market_add_two_sided_quotes(
+                self._h, bid_px.data_ptr(), bid_sz.data_ptr(), ask_px.data_ptr(), ask_sz.data_ptr(),
+                customer_ids.data_ptr(), *fp, _raw_stream(self._device_index))
         if rc:
             _fatal(_native.last_error())
 

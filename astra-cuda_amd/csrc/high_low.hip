@@ -100,7 +100,7 @@ ASTRA_HD void trade_post(const TradeArgs &a, int64_t n) {
   const int32_t cnt = t.fill_counts[n];
   int32_t last = t.last_prices[n];
   if (cnt > 0 && cnt <= a.F) {
-    last = t.fill_prices[n * a.F + (cnt - 1)];
+    last = t.fill_rows ? t.fill_rows[(n * a.F + (cnt - 1)) * 8] : t.fill_prices[n * a.F + (cnt - 1)];
     t.last_prices[n] = last;
   }
   // telemetry (:284-288)
@@ -264,14 +264,19 @@ int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *st
   const void *need[] = {t->move, t->columns, t->player_last_positions, t->target_positions,
                         t->contract_values, t->player_contract_over_time,
                         t->market_contract_over_time, t->immediate_rewards,
-                        t->rewards_since_last_action, t->fill_prices, t->fill_sizes,
-                        t->fill_customer_ids, t->fill_quoter_ids, t->fill_is_sell_quote,
-                        t->fill_quote_sizes, t->fill_tid, t->fill_quote_tid, t->fill_counts,
-                        t->best_bid_prices, t->best_bid_sizes, t->best_ask_prices,
-                        t->best_ask_sizes, t->last_prices, t->errors};
+                        t->rewards_since_last_action, t->fill_counts, t->best_bid_prices,
+                        t->best_bid_sizes, t->best_ask_prices, t->best_ask_sizes,
+                        t->last_prices, t->errors};
   for (const void *p : need)
     if (M > 0 && p == nullptr)
       return fail(ASTRA_ERR_INVALID_ARGUMENT, "astra_high_low_trade: null pointer in astra_hl_trade");
+  const void *fields[] = {t->fill_prices, t->fill_sizes, t->fill_customer_ids, t->fill_quoter_ids,
+                          t->fill_is_sell_quote, t->fill_quote_sizes, t->fill_tid,
+                          t->fill_quote_tid};
+  if (!t->fill_rows)
+    for (const void *p : fields)
+      if (M > 0 && p == nullptr)
+        return fail(ASTRA_ERR_INVALID_ARGUMENT, "astra_high_low_trade: null fill pointer");
   TradeArgs a;
   a.t = *t;
   a.N = M;
@@ -291,12 +296,18 @@ int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *st
     if (bits) return fail(ASTRA_ERR_INVALID_ARGUMENT, std::string("high_low_trading.cc ") + check_text(bits));
   }
   const int64_t N = M;
-  if ((rc = astra_market_add_two_sided_quotes(
-           market, t->columns, t->columns + N, t->columns + 2 * N, t->columns + 3 * N,
-           t->columns + 4 * N, t->fill_prices, t->fill_sizes, t->fill_customer_ids,
-           t->fill_quoter_ids, t->fill_is_sell_quote, t->fill_quote_sizes, t->fill_tid,
-           t->fill_quote_tid, t->fill_counts, stream)))
-    return rc;
+  if (t->fill_rows)
+    rc = astra_market_add_two_sided_quotes_rows(market, t->columns, t->columns + N,
+                                                t->columns + 2 * N, t->columns + 3 * N,
+                                                t->columns + 4 * N, t->fill_rows, t->fill_counts,
+                                                stream);
+  else
+    rc = astra_market_add_two_sided_quotes(
+        market, t->columns, t->columns + N, t->columns + 2 * N, t->columns + 3 * N,
+        t->columns + 4 * N, t->fill_prices, t->fill_sizes, t->fill_customer_ids,
+        t->fill_quoter_ids, t->fill_is_sell_quote, t->fill_quote_sizes, t->fill_tid,
+        t->fill_quote_tid, t->fill_counts, stream);
+  if (rc) return rc;
   return launch_post(a, s);
 }
 

@@ -148,10 +148,14 @@ struct QuoteIn {
   int32_t base_tid;
 };
 
+// Fill rows go either to the reference's eight [M,F] arrays or, when `rows` is
+// set, to one [M,F,8] int32 array: row (m, k) is 32 contiguous bytes {price,
+// size, taker, quoter, is_sell (0/1), quote size, tid, quote tid}.
 struct FillOut {
   int32_t *prices, *sizes, *taker, *quoter;
   uint8_t *is_sell_quote;
   int32_t *quote_sizes, *tid, *quote_tid, *counts;
+  int32_t *rows;
 };
 
 // ---- small device/host helpers ----
@@ -253,7 +257,17 @@ struct Bulk {
   int32_t v[8];   // price, size, taker, quoter, is_sell_quote, quote_size, tid, quote_tid
 };
 
+ASTRA_HD void write_row(int32_t *rows, int64_t fi, const int32_t (&v)[8]) {
+  int4 *d = reinterpret_cast<int4 *>(rows + fi * 8);
+  d[0] = make_int4(v[0], v[1], v[2], v[3]);
+  d[1] = make_int4(v[4], v[5], v[6], v[7]);
+}
+
 ASTRA_HD void write_fill(const FillOut &out, int64_t fi, const int32_t (&v)[8]) {
+  if (out.rows) {
+    write_row(out.rows, fi, v);
+    return;
+  }
   out.prices[fi] = v[0];
   out.sizes[fi] = v[1];
   out.taker[fi] = v[2];
@@ -316,6 +330,19 @@ struct FillSink {
 
   ASTRA_HD void flush(const FillOut &out, int32_t *pf, int32_t C) {
     if (n == 0) return;
+    if (out.rows) {
+      for (int r = 0; r < n; ++r) {
+        int32_t v[8];
+#pragma unroll
+        for (int f = 0; f < 8; ++f) v[f] = at(f, r);
+        write_row(out.rows, base + r, v);
+      }
+      for (int r = 0; r < n; ++r)
+        apply_portfolio(pf, C, at(0, r), at(1, r), at(2, r), at(3, r), at(4, r) != 0);
+      base += n;
+      n = 0;
+      return;
+    }
     int32_t *dst32[7] = {out.prices, out.sizes, out.taker, out.quoter, out.quote_sizes, out.tid,
                          out.quote_tid};
     const int fidx[7] = {0, 1, 2, 3, 5, 6, 7};
@@ -855,9 +882,9 @@ ASTRA_HD void bbo_copy_market(const Book &b, int32_t *bid_px, int32_t *bid_sz, i
 // update_last_prices_kernel (market.cu:767-786). A count above F (only possible
 // for caller-made fill_counts) leaves the last price unchanged.
 ASTRA_HD void last_price_market(int32_t *last, const int32_t *counts, const int32_t *prices,
-                                int32_t F, int64_t m) {
+                                int32_t F, int32_t stride, int64_t m) {
   const int32_t c = counts[m];
-  if (c > 0 && c <= F) last[m] = prices[m * (int64_t)F + (c - 1)];
+  if (c > 0 && c <= F) last[m] = prices[(m * (int64_t)F + (c - 1)) * stride];
 }
 
 // ClearQuotes (market.cu:735-749) for thread t = (market, level): the level's
@@ -1054,9 +1081,9 @@ __global__ __launch_bounds__(256) void bbo_kernel(Book b, int32_t *bid_px, int32
 
 __global__ __launch_bounds__(256) void last_price_kernel(int32_t *last, const int32_t *counts,
                                                          const int32_t *prices, int32_t M,
-                                                         int32_t F) {
+                                                         int32_t F, int32_t stride) {
   const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (m < M) last_price_market(last, counts, prices, F, m);
+  if (m < M) last_price_market(last, counts, prices, F, stride, m);
 }
 
 template <int W>
@@ -1203,13 +1230,13 @@ int launch_fill(void *dst, int64_t n_words, uint32_t v, hipStream_t s, const cha
 }
 
 int launch_last_price(int32_t *last, const int32_t *counts, const int32_t *prices, int32_t M,
-                      int32_t F, hipStream_t s) {
+                      int32_t F, int32_t stride, hipStream_t s) {
 #ifdef ASTRA_HOST_EMULATION
   (void)s;
-  for (int64_t m = 0; m < M; ++m) last_price_market(last, counts, prices, F, m);
+  for (int64_t m = 0; m < M; ++m) last_price_market(last, counts, prices, F, stride, m);
 #else
   hipLaunchKernelGGL(last_price_kernel, dim3(grid_for(M, 256)), dim3(256), 0, s, last, counts,
-                     prices, M, F);
+                     prices, M, F, stride);
 #endif
   ASTRA_HIP_CHECK(rt_last_error(), "UpdateLastPrices");
   return ASTRA_OK;
@@ -1399,7 +1426,33 @@ int astra_market_add_two_sided_quotes(astra_market *h, const int32_t *bid_px,
     const QuoteIn in{bid_px, bid_sz, ask_px, ask_sz, customer_ids, h->tid};
     const FillOut fo{fill_prices,        fill_sizes,       fill_customer_ids, fill_quoter_ids,
                      fill_is_sell_quote, fill_quote_sizes, fill_tid,          fill_quote_tid,
-                     fill_counts};
+                     fill_counts,        nullptr};
+    const int rc = [&]() -> int {
+      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match, h, in, fo, as_stream(stream));
+    }();
+    if (rc) return rc;
+  }
+  h->tid = (int32_t)((uint32_t)h->tid + 2u);  // market.cu:531
+  return ASTRA_OK;
+}
+
+int astra_market_add_two_sided_quotes_rows(astra_market *h, const int32_t *bid_px,
+                                           const int32_t *bid_sz, const int32_t *ask_px,
+                                           const int32_t *ask_sz, const int32_t *customer_ids,
+                                           int32_t *fill_rows, int32_t *fill_counts,
+                                           void *stream) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  if (h->M > 0) {
+    if (!bid_px || !bid_sz || !ask_px || !ask_sz || !customer_ids || !fill_counts)
+      return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL input or fill_counts pointer");
+    if (h->F > 0 && !fill_rows) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL fill_rows pointer");
+    if ((reinterpret_cast<uintptr_t>(fill_rows) & 15) != 0)
+      return fail(ASTRA_ERR_INVALID_ARGUMENT, "fill_rows must be 16-byte aligned");
+    DeviceGuard g(h->device);
+    const QuoteIn in{bid_px, bid_sz, ask_px, ask_sz, customer_ids, h->tid};
+    FillOut fo{};
+    fo.counts = fill_counts;
+    fo.rows = fill_rows;
     const int rc = [&]() -> int {
       ASTRA_DISPATCH_W(h->lay.W, launch_quote_match, h, in, fo, as_stream(stream));
     }();
@@ -1426,7 +1479,17 @@ int astra_update_last_prices(int32_t *last, const int32_t *counts, const int32_t
   if (M == 0) return ASTRA_OK;
   if (!last || !counts || (F > 0 && !prices))
     return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL pointer");
-  return launch_last_price(last, counts, prices, M, F, as_stream(stream));
+  return launch_last_price(last, counts, prices, M, F, 1, as_stream(stream));
+}
+
+int astra_update_last_prices_rows(int32_t *last, const int32_t *counts, const int32_t *fill_rows,
+                                  int32_t M, int32_t F, void *stream) {
+  ASTRA_ABI_CHECK(M, >=, 0);
+  ASTRA_ABI_CHECK(F, >=, 0);
+  if (M == 0) return ASTRA_OK;
+  if (!last || !counts || (F > 0 && !fill_rows))
+    return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL pointer");
+  return launch_last_price(last, counts, fill_rows, M, F, 8, as_stream(stream));
 }
 
 int astra_fill_i32(int32_t *dst, int64_t count, int32_t value, void *stream) {

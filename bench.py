@@ -16,7 +16,10 @@ pre-timed state, so they see exactly the same work):
      launches issued back to back (then around K get_bbos launches), so the
      mean per launch is the kernel's average duration;
   D  work counts: the diagnostic kernel variant counts inserts, fill rows and
-     emptied levels, for the algorithmic-byte roofline.
+     emptied levels, for the algorithmic-byte roofline;
+  R  the timed steps again with a FillBatch in the row layout
+     (new_fill_batch(layout="rows"), not the reference's), reported beside the
+     headline as value_rows_layout.
 Then the CPU baseline: the oracle (a C port of the reference algorithm) on a
 bounded subset of the same markets and steps, all host threads and 1 thread.
 
@@ -56,7 +59,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the all-thread oracle leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--phases", default="ABCD",
+    ap.add_argument("--phases", default="ABCDR",
                     help="phases to run (A is always run; B latency, C events, D work counts)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for rocprof counter scaling)")
@@ -142,7 +145,7 @@ def main():
     torch.cuda.synchronize()
     phases = set(args.phases.upper()) | {"A"}
     # state at the start of the timed steps, for the replays B, C and D
-    snaps = [market.clone() if p in phases else None for p in "BCD"]
+    snaps = [market.clone() if p in phases else None for p in "BCDR"]
     torch.cuda.synchronize()
     log(f"warm-up done ({W} steps); timing {K} steps")
 
@@ -198,6 +201,20 @@ def main():
         torch.cuda.synchronize()
         snaps[2]._set_stats(None)
     n_ins, n_fill, n_empty, n_ovf, n_ff = (int(x) for x in counters.cpu().tolist()[:5])
+
+    # ---- R: the same steps with the row layout of the FillBatch ----
+    wall_rows = None
+    if "R" in phases:
+        rfills = snaps[3].new_fill_batch(layout="rows")
+        torch.cuda.synchronize()
+        r0 = time.perf_counter()
+        for t in range(W, T):
+            snaps[3].add_two_sided_quotes(*rows[t], rfills)
+            if bbo:
+                snaps[3].get_bbos(bbos)
+        torch.cuda.synchronize()
+        wall_rows = time.perf_counter() - r0
+        log(f"R: {K} steps in {wall_rows * 1e3:.2f} ms with the row layout")
     log(f"work over {K} steps: inserts {n_ins}, fill rows {n_fill}, emptied {n_empty}, overflow {n_ovf}")
 
     # algorithmic bytes (per launch of the matching kernel): quotes in 20 B + fill_counts 4 B
@@ -229,6 +246,7 @@ def main():
             "get_bbos_every_step": bbo, "parallelism": "single GPU, one lane per market",
         },
         "market_steps_per_s": K / wall,
+        "value_rows_layout": (M * K / wall_rows) if wall_rows else None,
         "p50_step_latency_ms": float(np.percentile(lat_ms, 50)),
         "p99_step_latency_ms": float(np.percentile(lat_ms, 99)),
         "max_step_latency_ms": float(lat_ms.max()),

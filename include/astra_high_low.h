@@ -53,6 +53,9 @@ typedef struct astra_hl_trade {
   uint8_t *fill_is_sell_quote;
   int32_t *fill_quote_sizes, *fill_tid, *fill_quote_tid, *fill_counts;
   int32_t *best_bid_prices, *best_bid_sizes, *best_ask_prices, *best_ask_sizes, *last_prices;
+  int32_t *fill_rows;             /* non-NULL: the fills go to this [N,F,8] row array
+                                     (astra_market_add_two_sided_quotes_rows) and the
+                                     eight field pointers above are not used */
   int32_t *errors;                /* [1]: ASTRA_HL_ERR_* bits are OR-ed in; the caller zeroes it */
   int32_t players, steps_per_player, max_contracts_per_trade, max_contract_value;
   int32_t player;                 /* the acting player (CurrentPlayer) */

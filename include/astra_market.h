@@ -94,6 +94,18 @@ int astra_market_add_two_sided_quotes(astra_market *market, const int32_t *bid_p
                                       int32_t *fill_tid, int32_t *fill_quote_tid,
                                       int32_t *fill_counts, void *stream);
 
+/* astra_market_add_two_sided_quotes with the fill rows in one int32 [M, F, 8]
+ * array (16-byte aligned): row (m, k) = {price, size, taker, quoter, is_sell (0/1),
+ * quote size, tid, quote tid}, the eight FillBatch fields of market.h:64-92 side by
+ * side, so a row is one 32-byte write instead of eight scattered ones. No
+ * counterpart in the reference: an alternative layout of the same FillBatch
+ * (the Python layer exposes the eight fields as strided [M, F] views of it). */
+int astra_market_add_two_sided_quotes_rows(astra_market *market, const int32_t *bid_px,
+                                           const int32_t *bid_sz, const int32_t *ask_px,
+                                           const int32_t *ask_sz, const int32_t *customer_ids,
+                                           int32_t *fill_rows, int32_t *fill_counts,
+                                           void *stream);
+
 /* VecMarket::GetBBOs (market.cu:573-597): four int32 [M] outputs. The values
  * are those of the book as the last mutating call left it (the matching kernel
  * computes them; this call copies them out). */
@@ -105,6 +117,12 @@ int astra_market_get_bbos(const astra_market *market, int32_t *best_bid_prices,
 int astra_update_last_prices(int32_t *last_prices, const int32_t *fill_counts,
                              const int32_t *fill_prices, int32_t num_markets,
                              int32_t max_fills, void *stream);
+
+/* BBOBatch::UpdateLastPrices for a FillBatch in the row layout of
+ * astra_market_add_two_sided_quotes_rows. */
+int astra_update_last_prices_rows(int32_t *last_prices, const int32_t *fill_counts,
+                                  const int32_t *fill_rows, int32_t num_markets,
+                                  int32_t max_fills, void *stream);
 
 /* Fill `count` int32 words with `value` on `stream` (used for FillBatch::Reset,
  * market.cu:758-760, and BBOBatch::Reset, market.cu:788-796). */

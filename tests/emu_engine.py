@@ -80,6 +80,22 @@ class EmuFills:
         return [getattr(self, f).ctypes.data for f in self.FIELDS]
 
 
+class EmuRowFills:
+    """A FillBatch in the row layout: int32 [M, F, 8] rows plus fill_counts; the
+    fields read as views of the rows."""
+    FIELDS = EmuFills.FIELDS
+
+    def __init__(self, M, F):
+        self.rows = np.zeros((M, F, 8), np.int32)
+        self.fill_counts = np.zeros((M,), np.int32)
+
+    def __getattr__(self, name):
+        if name in self.FIELDS[:8]:
+            v = self.rows[:, :, self.FIELDS.index(name)]
+            return v.astype(np.bool_) if name == "fill_is_sell_quote" else v
+        raise AttributeError(name)
+
+
 class EmuBBO:
     FIELDS = ("best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes", "last_prices")
 
@@ -118,14 +134,19 @@ class EmuMarket:
     def clone(self):
         return EmuMarket(self.M, self.L, self.O, self.F, self.C, bool(self.flags), _src=self)
 
-    def new_fill_batch(self):
-        return EmuFills(self.M, self.F)
+    def new_fill_batch(self, layout="columns"):
+        return EmuRowFills(self.M, self.F) if layout == "rows" else EmuFills(self.M, self.F)
 
     def new_bbo_batch(self):
         return EmuBBO(self.M)
 
     def add_two_sided_quotes(self, bid_px, bid_sz, ask_px, ask_sz, cust, fills):
         ins = [np.ascontiguousarray(a, np.int32) for a in (bid_px, bid_sz, ask_px, ask_sz, cust)]
+        if isinstance(fills, EmuRowFills):
+            _check(lib().astra_market_add_two_sided_quotes_rows(
+                self.h, *[a.ctypes.data for a in ins], fills.rows.ctypes.data, fills.fill_counts.ctypes.data,
+                None))
+            return
         _check(lib().astra_market_add_two_sided_quotes(self.h, *[a.ctypes.data for a in ins],
                                                         *fills.ptrs(), None))
 
@@ -135,6 +156,10 @@ class EmuMarket:
                                            b.best_ask_sizes.ctypes.data, None))
 
     def update_last_prices(self, b, fills):
+        if isinstance(fills, EmuRowFills):
+            _check(lib().astra_update_last_prices_rows(b.last_prices.ctypes.data, fills.fill_counts.ctypes.data,
+                                                       fills.rows.ctypes.data, self.M, self.F, None))
+            return
         _check(lib().astra_update_last_prices(b.last_prices.ctypes.data, fills.fill_counts.ctypes.data,
                                               fills.fill_prices.ctypes.data, self.M, self.F, None))
 
@@ -168,9 +193,11 @@ class EmuMarket:
 class EmuAdapter:
     """KAT adapter (tests/kat_harness.py) over the emulation build."""
 
+    layout = "columns"
+
     def __init__(self, shape):
         self.mk = EmuMarket(shape["M"], shape["L"], shape["O"], shape["F"], shape["C"])
-        self.fills = self.mk.new_fill_batch()
+        self.fills = self.mk.new_fill_batch(self.layout)
         self.bbo = self.mk.new_bbo_batch()
 
     def quote(self, *args):
@@ -197,10 +224,14 @@ class EmuAdapter:
             return self.mk.portfolios.copy()
         if name in EmuBBO.FIELDS:
             return getattr(self.bbo, name).copy()
-        return getattr(self.fills, name).copy()
+        return np.array(getattr(self.fills, name))
 
     def to_string(self, m):
         return self.mk.to_string(m)
+
+
+class EmuRowAdapter(EmuAdapter):
+    layout = "rows"
 
 
 class EmuHighLow:
@@ -208,12 +239,12 @@ class EmuHighLow:
     with numpy arrays as the state tensors (high_low_trading.h:85-115). The setup
     arrays (contract values, settle flags, permutation, targets) are set directly."""
 
-    def __init__(self, N, P, T, S, cM, V, market_shape):
+    def __init__(self, N, P, T, S, cM, V, market_shape, layout="columns"):
         from astra_cuda._native import HLObservation, HLTrade
         self.N, self.P, self.T, self.S, self.cM, self.V = N, P, T, S, cM, V
         L, O, F, C = market_shape
         self.market = EmuMarket(N, L, O, F, C)
-        self.fills = self.market.new_fill_batch()
+        self.fills = self.market.new_fill_batch(layout)
         self.bbo = self.market.new_bbo_batch()
         z = lambda *s: np.zeros(s, np.int32)  # noqa: E731
         self.contract_values = z(N, 3)
@@ -238,8 +269,11 @@ class EmuHighLow:
                      "rewards_since_last_action", "errors"):
             setattr(t, name, ptr(getattr(self, name)))
         t.move = ptr(self.move)
-        for f in EmuFills.FIELDS:
-            setattr(t, f, ptr(getattr(self.fills, f)))
+        if isinstance(self.fills, EmuRowFills):
+            t.fill_rows, t.fill_counts = ptr(self.fills.rows), ptr(self.fills.fill_counts)
+        else:
+            for f in EmuFills.FIELDS:
+                setattr(t, f, ptr(getattr(self.fills, f)))
         for f in EmuBBO.FIELDS:
             setattr(t, f, ptr(getattr(self.bbo, f)))
         t.players, t.steps_per_player = self.P, self.T

@@ -16,13 +16,14 @@ def t32(a) -> torch.Tensor:
 
 class GpuAdapter:
     """KAT adapter over astra_cuda.order_matching (the product path)."""
+    layout = "columns"
 
     def __init__(self, shape):
         from astra_cuda import order_matching as aom
         ext = shape["L"] > 128 or shape["O"] > 1024 or shape["F"] > 1024 or shape["C"] > 1024
         self.mk = aom.VecMarket(shape["M"], shape["L"], shape["O"], shape["F"], shape["C"],
                                 allow_extended_shapes=ext)
-        self.fills = self.mk.new_fill_batch()
+        self.fills = self.mk.new_fill_batch(self.layout)
         self.bbo = self.mk.new_bbo_batch()
 
     def quote(self, bid_px, bid_sz, ask_px, ask_sz, cust):
@@ -53,6 +54,10 @@ class GpuAdapter:
 
     def to_string(self, m):
         return self.mk.to_string(m)
+
+
+class GpuRowAdapter(GpuAdapter):
+    layout = "rows"
 
 
 def effective_counts(counts: np.ndarray, F: int) -> np.ndarray:
@@ -128,7 +133,7 @@ def make_market(M, L, O, F, C, extended=None, stage_budget=None):
 
 
 def run_parity(M, L, O, F, C, steps, gen, *, bbo_every=1, full_every=0, last_every=1,
-               extended=None, nthreads=8, label="", stage_budget=None):
+               extended=None, nthreads=8, label="", stage_budget=None, layout="columns"):
     """Drive GPU engine and oracle with the same inputs; compare after every step.
 
     ``gen(t)`` returns (bid_px, bid_sz, ask_px, ask_sz, cust) int32 arrays of shape [M].
@@ -136,7 +141,7 @@ def run_parity(M, L, O, F, C, steps, gen, *, bbo_every=1, full_every=0, last_eve
     """
     from oracle.oracle import OracleMarket
     g = make_market(M, L, O, F, C, extended, stage_budget)
-    gf, gb = g.new_fill_batch(), g.new_bbo_batch()
+    gf, gb = g.new_fill_batch(layout), g.new_bbo_batch()
     o = OracleMarket(M, L, O, F, C)
     of, ob = o.new_fill_batch(), o.new_bbo_batch()
     rows = overflows = 0

@@ -11,7 +11,7 @@ import os
 import numpy as np
 import pytest
 
-from emu_engine import EmuAdapter, EmuMarket
+from emu_engine import EmuAdapter, EmuMarket, EmuRowAdapter
 from kat_harness import FILL_FIELDS, load_kats, run_scenario
 from oracle.oracle import OracleMarket
 
@@ -19,8 +19,9 @@ SCENARIOS = load_kats()
 
 
 @pytest.mark.parametrize("sc", SCENARIOS, ids=[s["name"] for s in SCENARIOS])
-def test_emulated_kat(sc):
-    run_scenario(sc, EmuAdapter)
+@pytest.mark.parametrize("adapter", [EmuAdapter, EmuRowAdapter], ids=["columns", "rows"])
+def test_emulated_kat(sc, adapter):
+    run_scenario(sc, adapter)
 
 
 def _compare(em, ef, eb, om, of, ob, F, where):
@@ -52,9 +53,9 @@ def _emu(M, L, O, F, C, stage_budget=None):
             os.environ["ASTRA_MARKET_STAGE_BUDGET"] = old
 
 
-def _run(M, L, O, F, C, steps, gen, with_stats=False, stage_budget=None):
+def _run(M, L, O, F, C, steps, gen, with_stats=False, stage_budget=None, layout="columns"):
     em, om = _emu(M, L, O, F, C, stage_budget), OracleMarket(M, L, O, F, C)
-    ef, of = em.new_fill_batch(), om.new_fill_batch()
+    ef, of = em.new_fill_batch(layout), om.new_fill_batch()
     eb, ob = em.new_bbo_batch(), om.new_bbo_batch()
     stats = np.zeros(8, np.int64)
     ostats = {"inserts": 0, "fills": 0, "levels_emptied": 0, "overflows": 0}
@@ -92,9 +93,10 @@ ALIAS_CASES = [
 ]
 
 
-@pytest.mark.parametrize("stage_budget", [None, 0, 1, 3])
+@pytest.mark.parametrize("stage_budget,layout", [(None, "columns"), (0, "columns"), (1, "columns"),
+                                                 (3, "columns"), (None, "rows"), (1, "rows")])
 @pytest.mark.parametrize("M,L,O,F,C,steps,seed", ALIAS_CASES)
-def test_emulated_aliasing_vs_oracle(M, L, O, F, C, steps, seed, stage_budget):
+def test_emulated_aliasing_vs_oracle(M, L, O, F, C, steps, seed, stage_budget, layout):
     rng = np.random.default_rng(seed)
     hot = max(4, min(L, 24))
 
@@ -107,7 +109,7 @@ def test_emulated_aliasing_vs_oracle(M, L, O, F, C, steps, seed, stage_budget):
         return (bid, rng.integers(-1, 8, M).astype(np.int32), ask,
                 rng.integers(-1, 8, M).astype(np.int32), rng.integers(-1, C + 2, M).astype(np.int32))
 
-    _, _, st = _run(M, L, O, F, C, steps, gen, with_stats=True, stage_budget=stage_budget)
+    _, _, st = _run(M, L, O, F, C, steps, gen, with_stats=True, stage_budget=stage_budget, layout=layout)
     # tiny rings exercise both overflow routes: the repeating-state fast-forward
     # and the ordinary F-th fill (with O = 1 every overflow repeats)
     assert st["fast_forwards"] > 0
@@ -123,13 +125,14 @@ def test_emulated_config1_full_run():
     assert st["fills"] > 0
 
 
-@pytest.mark.parametrize("stage_budget", [None, 1])
-def test_emulated_config3_and_4_samples(stage_budget):
+@pytest.mark.parametrize("stage_budget,layout", [(None, "columns"), (1, "columns"), (1, "rows")])
+def test_emulated_config3_and_4_samples(stage_budget, layout):
     from astra_cuda.workloads import CONFIGS, QuoteStream
     for idx, M, steps in ((3, 300, 700), (4, 60, 400)):
         cfg = CONFIGS[idx]
         qs = QuoteStream(cfg, np.arange(M))
-        _run(M, cfg.L, cfg.O, cfg.F, cfg.C, steps, qs.step, with_stats=True, stage_budget=stage_budget)
+        _run(M, cfg.L, cfg.O, cfg.F, cfg.C, steps, qs.step, with_stats=True, stage_budget=stage_budget,
+             layout=layout)
 
 
 def test_emulated_reset_clear_clone_to_string():

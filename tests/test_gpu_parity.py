@@ -10,7 +10,8 @@ import pytest
 import torch
 
 from kat_harness import load_kats, run_scenario
-from parity_util import DEV, GpuAdapter, compare_bbo, compare_fills, compare_portfolios, run_parity, t32
+from parity_util import (DEV, GpuAdapter, GpuRowAdapter, compare_bbo, compare_fills, compare_portfolios,
+                         run_parity, t32)
 
 pytestmark = pytest.mark.gpu
 
@@ -22,9 +23,10 @@ def _log(msg):
 
 
 @pytest.mark.parametrize("sc", SCENARIOS, ids=[s["name"] for s in SCENARIOS])
-def test_gpu_kat(sc):
-    _log(f"kat {sc['name']}")
-    run_scenario(sc, GpuAdapter)
+@pytest.mark.parametrize("adapter", [GpuAdapter, GpuRowAdapter], ids=["columns", "rows"])
+def test_gpu_kat(sc, adapter):
+    _log(f"kat {sc['name']} {adapter.layout}")
+    run_scenario(sc, adapter)
 
 
 def test_gpu_library_is_the_in_tree_build():
@@ -56,15 +58,15 @@ def test_gpu_config2_subset():
     assert r["fill_rows"] > 3000
 
 
-@pytest.mark.parametrize("stage_budget", [None, 1])
-def test_gpu_config3_subset_with_eviction(stage_budget):
+@pytest.mark.parametrize("stage_budget,layout", [(None, "columns"), (1, "columns"), (None, "rows")])
+def test_gpu_config3_subset_with_eviction(stage_budget, layout):
     """Config 3 markets 0..3999 for all 1000 steps (the ring of 1024 wraps after 512 steps).
     With stage_budget=1 every market that crosses twice in a call finishes on the
     LDS-staged path."""
     cfg, gen = _stream_gen(3, np.arange(4000))
-    _log(f"config 3 subset: 4000 x 1000, stage budget {stage_budget}")
+    _log(f"config 3 subset: 4000 x 1000, stage budget {stage_budget}, {layout}")
     r = run_parity(4000, cfg.L, cfg.O, cfg.F, cfg.C, 1000, gen, bbo_every=1, full_every=250,
-                   label="cfg3", stage_budget=stage_budget)
+                   label="cfg3", stage_budget=stage_budget, layout=layout)
     assert r["fill_rows"] > 4000
 
 
@@ -92,10 +94,10 @@ ALIAS_CASES = [
 ]
 
 
-@pytest.mark.parametrize("stage_budget", [None, 1])
+@pytest.mark.parametrize("stage_budget,layout", [(None, "columns"), (1, "columns"), (1, "rows")])
 @pytest.mark.parametrize("M,L,O,F,C,steps,seed", ALIAS_CASES)
-def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget):
-    _log(f"aliasing M={M} L={L} O={O} F={F} stage budget {stage_budget}")
+def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, layout):
+    _log(f"aliasing M={M} L={L} O={O} F={F} stage budget {stage_budget} {layout}")
     rng = np.random.default_rng(seed)
     hot = max(4, min(L, 24))  # concentrate prices so books cross often
 
@@ -109,7 +111,7 @@ def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget):
                 rng.integers(-1, 8, M).astype(np.int32), rng.integers(-1, C + 2, M).astype(np.int32))
 
     r = run_parity(M, L, O, F, C, steps, gen, full_every=50, label=f"alias L{L} O{O}",
-                   stage_budget=stage_budget)
+                   stage_budget=stage_budget, layout=layout)
     if O <= 3:
         assert r["overflows"] > 0
 
@@ -229,3 +231,35 @@ def test_gpu_input_validation_errors():
         g.clear_quotes(torch.zeros(4, dtype=torch.int32, device=DEV))
     # no state change from the rejected calls: TID still 0
     assert g.global_tid == 0
+
+
+def test_gpu_row_layout_fill_batch():
+    """FillBatch(layout="rows"): the fields are [M, F] views of one [M, F, 8] buffer with
+    the dtypes of the reference; clone keeps the layout; assigning a field leaves it."""
+    from astra_cuda import order_matching as aom
+    M, F = 7, 5
+    g = aom.VecMarket(M, 32, 16, F, 4)
+    fr, fc = g.new_fill_batch(layout="rows"), g.new_fill_batch()
+    assert fr.layout == "rows" and fc.layout == "columns"
+    for f in aom.FillBatch.FIELDS:
+        a, b = getattr(fr, f), getattr(fc, f)
+        assert a.shape == b.shape and a.dtype == b.dtype, f
+    one = torch.ones(M, dtype=torch.int32, device=DEV)
+    for fills in (fr, fc):
+        g2 = aom.VecMarket(M, 32, 16, F, 4)
+        g2.add_two_sided_quotes(one * 10, one * 3, one * 20, one * 2, one * 0, fills)
+        g2.add_two_sided_quotes(one * 20, one * 5, one * 10, one * 4, one * 1, fills)
+    for f in aom.FillBatch.FIELDS:
+        assert torch.equal(getattr(fr, f), getattr(fc, f)), f
+    assert fr.fill_is_sell_quote.any() or not fc.fill_is_sell_quote.any()
+    b1, b2 = g.new_bbo_batch(), g.new_bbo_batch()
+    b1.update_last_prices(fr)
+    b2.update_last_prices(fc)
+    assert torch.equal(b1.last_prices, b2.last_prices) and b1.last_prices.tolist() == [20] * M
+    cl = fr.clone()
+    assert cl.layout == "rows" and torch.equal(cl.fill_prices, fr.fill_prices)
+    assert cl.fill_prices.data_ptr() != fr.fill_prices.data_ptr()
+    fr.fill_sizes = torch.zeros((M, F), dtype=torch.int32, device=DEV)
+    assert fr.layout == "columns"
+    with pytest.raises(RuntimeError, match="must be contiguous"):
+        g.add_two_sided_quotes(one, one, one, one, one * 0, fr)

@@ -29,10 +29,10 @@ def _compare(o, e, where):
     assert np.array_equal(o.fills.fill_counts, e.fills.fill_counts), where
 
 
-def _play(N, P, T, S, cM, V, shape, seed, obs_every=3):
+def _play(N, P, T, S, cM, V, shape, seed, obs_every=3, layout="columns"):
     rng = np.random.default_rng(seed)
     o = OracleHighLow(N, P, T, S, cM, V, market_shape=shape)
-    e = EmuHighLow(N, P, T, S, cM, V, (o.L, o.O, o.F, o.C))
+    e = EmuHighLow(N, P, T, S, cM, V, (o.L, o.O, o.F, o.C), layout)
     chance, moves = random_game(rng, N, P, T, S, cM, V)
     for c in chance:
         o.apply_action(c)
@@ -54,8 +54,9 @@ def _play(N, P, T, S, cM, V, shape, seed, obs_every=3):
     (50, 5, 8, 3, 4, 20, (21, 12, 6, 5), 3),  # a ring of 12 wraps: slot reuse
     (40, 6, 4, 5, 5, 127, (128, 1024, 10, 16), 4),  # the config-5 shape (C > players)
 ])
-def test_emulated_game_vs_oracle(N, P, T, S, cM, V, shape, seed):
-    _play(N, P, T, S, cM, V, shape, seed)
+@pytest.mark.parametrize("layout", ["columns", "rows"])
+def test_emulated_game_vs_oracle(N, P, T, S, cM, V, shape, seed, layout):
+    _play(N, P, T, S, cM, V, shape, seed, layout=layout)
 
 
 def test_emulated_hand_game():
