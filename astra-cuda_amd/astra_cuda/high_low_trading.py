@@ -409,6 +409,115 @@ class HighLowTradingState:
                 "market": self.market_contract_over_time.clone(),
                 "target_positions": self.target_positions.clone()}
 
+    # ---- text renderings (:398-466, :603-804); copies the tensors to the host ----
+    def to_string(self, index: int = 0) -> str:
+        """ToString (:398-466)."""
+        self._check_index(index)
+        mn = self._move_number
+        out = ["********** Game setup **********\n"]
+        if mn >= 1:
+            cv = self.contract_values[index].tolist()
+            out.append(f"Contract values: {cv[0]}, {cv[1]}\n")
+        if mn >= 2:
+            out.append("Contract high settle: " + ("High" if bool(self.contract_high_settle[index]) else "Low") + "\n")
+        if mn >= 3:
+            roles = [f"P{i}=" + ("ValueCheater" if r in (0, 1) else "HighLowCheater" if r == 2 else "Customer")
+                     for i, r in enumerate(self.player_permutation[index].tolist())]
+            out.append("Player permutation: Player roles: " + ", ".join(roles) + "\n")
+        if mn >= 4:
+            for i, t in enumerate(self.target_positions[index].tolist()):
+                out.append(f"Player {i} target position: " + ("No requirement" if t == 0 else str(t)) + "\n")
+        out.append("********************************\n\n")
+        if mn >= MAX_CHANCE_NODES:
+            out.append(self._public_information_string(index))
+        return "".join(out)
+
+    def information_state_string(self, player: int | None = None, index: int = 0) -> str:
+        """InformationStateString (:620-680). Called with one positional argument it
+        is the player, as the reference binding resolves its two overloads
+        (core_bindings.cc:59-64); without a player it uses the current player."""
+        if player is None:
+            player = self.current_player()
+        player, index = int(player), int(index)
+        _assert(0 <= player < self._P, f"player >= 0 && player < NumPlayers()\nplayer = {player}")
+        self._check_index(index)
+        out = ["********** Private Information **********\n"]
+        if self._move_number >= MAX_CHANCE_NODES:
+            perm = int(self.player_permutation[index, player])
+            role = "ValueCheater" if perm in (0, 1) else "HighLowCheater" if perm == 2 else "Customer"
+            out.append(f"My role: {role}\n")
+            if perm in (0, 1):
+                out.append(f"Candidate contract value: {int(self.contract_values[index, perm])}\n")
+            elif perm == 2:
+                out.append("Settlement will be: " + ("High" if bool(self.contract_high_settle[index]) else "Low") + "\n")
+            else:
+                t = int(self.target_positions[index, player])
+                if t == 0:
+                    _fatal("Not supposed to happen. Customer roles should be assigned")
+                out.append(f"My target position: {t}\n")
+            out.append("******************************************\n\n")
+            out.append(self._public_information_string(index))
+        else:
+            out.append("Private info pending...\n")
+            out.append("***************************\n")
+        return "".join(out)
+
+    observation_string = information_state_string  # ObservationString (:502-504)
+
+    def _public_information_string(self, index: int) -> str:
+        """PublicInformationString (:682-804)."""
+        g = self._game
+        out = ["********** Game Configuration **********\n", f"Environment: {index} / {self._N}\n",
+               f"Steps per player: {self._T}\n", f"Max contracts per trade: {g.max_contracts_per_trade}\n",
+               f"Customer max size: {g.customer_max_size}\n", f"Max contract value: {g.max_contract_value}\n",
+               f"Number of players: {self._P}\n", "****************************************\n\n",
+               "********** Player Positions **********\n"]
+        pf = self.market.get_customer_portfolios()[index].tolist()
+        for i in range(self._P):
+            out.append(f"Player {i} position: [{pf[i][0]} contracts, {pf[i][1]} cash]\n")
+        out.append("**************************************\n\n")
+        out.append("********** Quotes & Market Movement **********\n")
+        fb = self.fill_batch
+        n = int(fb.fill_counts[index])
+        out.append(f"Number of fills in the last round: {n}\n")
+        if n > 0:
+            cols = {f: getattr(fb, f)[index, :n].tolist() for f in (
+                "fill_prices", "fill_sizes", "fill_customer_ids", "fill_quoter_ids", "fill_is_sell_quote",
+                "fill_quote_sizes", "fill_tid", "fill_quote_tid")}
+            for i in range(n):
+                sell = bool(cols["fill_is_sell_quote"][i])
+                out.append(f"Order fill: id={cols['fill_customer_ids'][i]} {'bought' if sell else 'sold'} "
+                           f"{cols['fill_sizes'][i]} contracts at px={cols['fill_prices'][i]} on "
+                           f"t={cols['fill_tid'][i]}. Quote: id={cols['fill_quoter_ids'][i]} "
+                           f"{'sale' if sell else 'bid'} sz={cols['fill_quote_sizes'][i]}, "
+                           f"submitted t={cols['fill_quote_tid'][i]}\n")
+        ctm = max(0, self._move_number - MAX_CHANCE_NODES)
+        cr, pin = ctm // self._P, ctm % self._P
+        pc = self.player_contract_over_time[index].tolist()
+        for rnd in range(0, min(cr, self._T - 1) + 1):
+            for p in range(self._P if rnd < cr else pin):
+                bp, ap, bs, az = pc[p][rnd][:4]
+                if bp > 0 or ap > 0:
+                    out.append(f"Player {p} quote: {bp} @ {ap} [{bs} x {az}]\n")
+        out.append("\n--- Market Movement ---\n")
+        mc = self.market_contract_over_time[index].tolist()
+        for t in range(min(ctm, self._P * self._T)):
+            bb, ba, lp = mc[t]
+            out.append(f"Time {t}: Bid: {'none' if bb == -1 else bb} @ Ask: {'none' if ba == -1 else ba}"
+                       + (f", Last: {lp}" if lp != -1 else "") + "\n")
+        out.append("***********************************\n\n")
+        out.append("********** Current Market **********\n")
+        out.append(self.market.to_string(index))
+        return "".join(out)
+
+    def _check_index(self, index: int) -> None:
+        _assert(0 <= index < self._N, f"index >= 0 && index < num_envs_\nindex = {index}")
+
+    def __str__(self):
+        return self.to_string(0)
+
+    __repr__ = __str__
+
     def get_contract_value(self) -> torch.Tensor:  # :469-473
         _assert(self._move_number >= 2, "MoveNumber() >= 2")
         return self.contract_values[:, 2]
@@ -424,3 +533,6 @@ class HighLowTradingState:
     FillObservationTensor = fill_observation_tensor
     Clone = clone
     Reset = reset
+    ToString = to_string
+    InformationStateString = information_state_string
+    ObservationString = observation_string

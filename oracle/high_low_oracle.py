@@ -14,7 +14,9 @@ arrays wrap like torch's int32 kernels), on top of the C market oracle
 * the trading move (:247-329), including its input checks (:260-271);
 * FillRewards / FillRewardsSinceLastAction / FillReturns (:331-373);
 * DoReset (:375-394), IsTerminal (:465-467), ExposeInfo (:475-485);
-* FillObservationTensor (:510-602) in float32.
+* FillObservationTensor (:510-602) in float32;
+* the text renderings ToString (:398-466), InformationStateString (:620-680) and
+  PublicInformationString (:682-804), as module functions.
 
 The market shape defaults to the game's own (:57-69): L = max_contract_value + 1,
 O = players * steps_per_player * 2, F = min(O, 2 * max_contracts_per_trade),
@@ -260,3 +262,94 @@ class OracleHighLow:
         v[:, o + 3] = self.bbo.best_ask_sizes.astype(np.float32)
         v[:, o + 4] = self.bbo.last_prices.astype(np.float32)
         return v
+
+
+# ---- text renderings (high_low_trading.cc:398-466, 603-804), numpy restatement ----
+def _roles_line(perm_row):
+    names = []
+    for i, r in enumerate(perm_row):
+        names.append(f"P{i}=" + ("ValueCheater" if r in (0, 1) else "HighLowCheater" if r == 2 else "Customer"))
+    return "Player permutation: Player roles: " + ", ".join(names) + "\n"
+
+
+def oracle_to_string(o: OracleHighLow, index: int) -> str:
+    out = ["********** Game setup **********\n"]
+    mn = o.move_number
+    if mn >= 1:
+        out.append(f"Contract values: {o.contract_values[index, 0]}, {o.contract_values[index, 1]}\n")
+    if mn >= 2:
+        out.append("Contract high settle: " + ("High" if o.contract_high_settle[index] else "Low") + "\n")
+    if mn >= 3:
+        out.append(_roles_line(o.player_permutation[index]))
+    if mn >= 4:
+        for i in range(o.P):
+            t = int(o.target_positions[index, i])
+            out.append(f"Player {i} target position: " + ("No requirement" if t == 0 else str(t)) + "\n")
+    out.append("********************************\n\n")
+    if mn >= MAX_CHANCE_NODES:
+        out.append(oracle_public_information(o, index))
+    return "".join(out)
+
+
+def oracle_public_information(o: OracleHighLow, index: int) -> str:
+    out = ["********** Game Configuration **********\n",
+           f"Environment: {index} / {o.N}\n", f"Steps per player: {o.T}\n",
+           f"Max contracts per trade: {o.S}\n", f"Customer max size: {o.cM}\n",
+           f"Max contract value: {o.V}\n", f"Number of players: {o.P}\n",
+           "****************************************\n\n", "********** Player Positions **********\n"]
+    pf = o.market.customer_portfolios
+    for i in range(o.P):
+        out.append(f"Player {i} position: [{pf[index, i, 0]} contracts, {pf[index, i, 1]} cash]\n")
+    out.append("**************************************\n\n")
+    out.append("********** Quotes & Market Movement **********\n")
+    f = o.fills
+    n = int(f.fill_counts[index])
+    out.append(f"Number of fills in the last round: {n}\n")
+    for i in range(max(n, 0)):
+        sell = bool(f.fill_is_sell_quote[index, i])
+        out.append(f"Order fill: id={f.fill_customer_ids[index, i]} {'bought' if sell else 'sold'} "
+                   f"{f.fill_sizes[index, i]} contracts at px={f.fill_prices[index, i]} on t={f.fill_tid[index, i]}. "
+                   f"Quote: id={f.fill_quoter_ids[index, i]} {'sale' if sell else 'bid'} sz={f.fill_quote_sizes[index, i]}, "
+                   f"submitted t={f.fill_quote_tid[index, i]}\n")
+    ctm = max(0, o.move_number - MAX_CHANCE_NODES)
+    cr, pin = ctm // o.P, ctm % o.P
+    pc = o.player_contract_over_time
+    for rnd in range(0, min(cr, o.T - 1) + 1):
+        if rnd > cr:
+            break
+        for p in range(o.P if rnd < cr else pin):
+            bp, ap, bs, az = (int(x) for x in pc[index, p, rnd, :4])
+            if bp > 0 or ap > 0:
+                out.append(f"Player {p} quote: {bp} @ {ap} [{bs} x {az}]\n")
+    out.append("\n--- Market Movement ---\n")
+    mc = o.market_contract_over_time
+    for t in range(min(ctm, o.P * o.T)):
+        bb, ba, lp = (int(x) for x in mc[index, t])
+        out.append(f"Time {t}: Bid: {'none' if bb == -1 else bb} @ Ask: {'none' if ba == -1 else ba}"
+                   + (f", Last: {lp}" if lp != -1 else "") + "\n")
+    out.append("***********************************\n\n")
+    out.append("********** Current Market **********\n")
+    out.append(o.market.to_string(index))
+    return "".join(out)
+
+
+def oracle_information_state_string(o: OracleHighLow, player: int, index: int) -> str:
+    out = ["********** Private Information **********\n"]
+    if o.move_number >= MAX_CHANCE_NODES:
+        perm = int(o.player_permutation[index, player])
+        role = "ValueCheater" if perm in (0, 1) else "HighLowCheater" if perm == 2 else "Customer"
+        out.append(f"My role: {role}\n")
+        if perm in (0, 1):
+            out.append(f"Candidate contract value: {o.contract_values[index, perm]}\n")
+        elif perm == 2:
+            out.append("Settlement will be: " + ("High" if o.contract_high_settle[index] else "Low") + "\n")
+        else:
+            t = int(o.target_positions[index, player])
+            _check(t != 0, "Not supposed to happen. Customer roles should be assigned")
+            out.append(f"My target position: {t}\n")
+        out.append("******************************************\n\n")
+        out.append(oracle_public_information(o, index))
+    else:
+        out.append("Private info pending...\n")
+        out.append("***************************\n")
+    return "".join(out)

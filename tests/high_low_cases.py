@@ -62,3 +62,54 @@ def random_game(rng, N, P, T, S, cM, V):
         moves.append(np.stack([bid, ask, rng.integers(0, S + 1, N), rng.integers(0, S + 1, N)],
                               1).astype(np.int32))
     return [cand, hl, perm, cs], moves
+
+
+# Text of the hand game after move 3 (move number 8), worked out from
+# high_low_trading.cc:398-466 and :620-804; the market's own book text follows the
+# "Current Market" banner (pinned by the string_representation known-answer test).
+HAND_TEXT_AFTER = 3
+HAND_SETUP_TEXT = (
+    "********** Game setup **********\n"
+    "Contract values: 10, 20\n"
+    "Contract high settle: High\n"
+    "Player permutation: Player roles: P0=ValueCheater, P1=ValueCheater, P2=HighLowCheater, P3=Customer\n"
+    "Player 0 target position: No requirement\n"
+    "Player 1 target position: No requirement\n"
+    "Player 2 target position: No requirement\n"
+    "Player 3 target position: 2\n"
+    "********************************\n\n")
+HAND_PUBLIC_TEXT = (
+    "********** Game Configuration **********\n"
+    "Environment: 0 / 1\n"
+    "Steps per player: 2\n"
+    "Max contracts per trade: 5\n"
+    "Customer max size: 5\n"
+    "Max contract value: 30\n"
+    "Number of players: 4\n"
+    "****************************************\n\n"
+    "********** Player Positions **********\n"
+    "Player 0 position: [-1 contracts, 18 cash]\n"
+    "Player 1 position: [0 contracts, 7 cash]\n"
+    "Player 2 position: [0 contracts, 0 cash]\n"
+    "Player 3 position: [1 contracts, -25 cash]\n"
+    "**************************************\n\n"
+    "********** Quotes & Market Movement **********\n"
+    "Number of fills in the last round: 2\n"
+    "Order fill: id=3 sold 1 contracts at px=26 on t=7. Quote: id=3 bid sz=2, submitted t=6\n"
+    "Order fill: id=3 bought 1 contracts at px=25 on t=6. Quote: id=1 sale sz=1, submitted t=3\n"
+    "Player 0 quote: 12 @ 18 [2 x 1]\n"
+    "Player 1 quote: 18 @ 25 [3 x 1]\n"
+    "Player 2 quote: 10 @ 30 [0 x 0]\n"
+    "Player 3 quote: 26 @ 24 [2 x 1]\n"
+    "\n--- Market Movement ---\n"
+    "Time 0: Bid: 12 @ Ask: 18, Last: 0\n"
+    "Time 1: Bid: 18 @ Ask: 25, Last: 18\n"
+    "Time 2: Bid: 18 @ Ask: 25, Last: 18\n"
+    "Time 3: Bid: 18 @ Ask: none, Last: 25\n"
+    "***********************************\n\n"
+    "********** Current Market **********\n")
+HAND_PRIVATE_TEXT = {
+    0: "My role: ValueCheater\nCandidate contract value: 10\n",
+    2: "My role: HighLowCheater\nSettlement will be: High\n",
+    3: "My role: Customer\nMy target position: 2\n",
+}

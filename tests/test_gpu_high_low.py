@@ -131,3 +131,43 @@ def test_gpu_move_checks():
     with pytest.raises(RuntimeError, match="ask_sizes <= max_contracts_per_trade"):
         s2.check_errors()
     s2.check_errors()  # cleared
+
+
+def test_gpu_text_renderings():
+    """to_string / observation_string / information_state_string: the hand-derived
+    text, and the oracle's on a random game (every few moves, several envs)."""
+    from high_low_cases import HAND_PRIVATE_TEXT, HAND_PUBLIC_TEXT, HAND_SETUP_TEXT, HAND_TEXT_AFTER
+    from oracle.high_low_oracle import oracle_information_state_string, oracle_to_string
+    s = _game(HAND_GAME["params"]).new_initial_state()
+    assert s.observation_string(0) == ("********** Private Information **********\nPrivate info pending...\n"
+                                       "***************************\n")
+    for c in HAND_GAME["chance"]:
+        s.apply_action(_t(c))
+    for mv in HAND_GAME["moves"][:HAND_TEXT_AFTER + 1]:
+        s.apply_action(_t(np.array([mv], np.int32)))
+    book = s.market.to_string(0)
+    assert s.to_string(0) == HAND_SETUP_TEXT + HAND_PUBLIC_TEXT + book
+    assert str(s) == s.to_string(0)
+    for p, priv in HAND_PRIVATE_TEXT.items():
+        exp = ("********** Private Information **********\n" + priv +
+               "******************************************\n\n" + HAND_PUBLIC_TEXT + book)
+        assert s.observation_string(p, 0) == exp
+        assert s.information_state_string(p) == exp
+    # random game against the oracle
+    N, P, T, S, cM, V = 40, 5, 3, 5, 5, 30
+    rng = np.random.default_rng(9)
+    o = OracleHighLow(N, P, T, S, cM, V)
+    s = _game(_params(N, P, T, S, cM, V, None)).new_initial_state()
+    chance, moves = random_game(rng, N, P, T, S, cM, V)
+    for k, c in enumerate(chance):
+        o.apply_action(c)
+        s.apply_action(_t(c))
+        assert s.to_string(k) == oracle_to_string(o, k)
+    for k, mv in enumerate(moves):
+        o.apply_action(mv)
+        s.apply_action(_t(mv))
+        if k % 4 == 0 or k == len(moves) - 1:
+            for idx in (0, 7, N - 1):
+                assert s.to_string(idx) == oracle_to_string(o, idx), (k, idx)
+                for p in range(P):
+                    assert s.observation_string(p, idx) == oracle_information_state_string(o, p, idx), (k, idx, p)

@@ -72,3 +72,22 @@ def test_input_checks_stop_before_trading():
     with pytest.raises(GameError, match="ask_prices <= max_contract_value"):
         o.apply_action(bad)
     assert o.move_number == 4 and o.market.global_tid == 0
+
+
+def test_oracle_text_renderings():
+    from high_low_cases import (HAND_PRIVATE_TEXT, HAND_PUBLIC_TEXT, HAND_SETUP_TEXT, HAND_TEXT_AFTER)
+    from oracle.high_low_oracle import oracle_information_state_string, oracle_to_string
+    o = OracleHighLow(**HAND_GAME["params"])
+    pending = oracle_information_state_string(o, 0, 0)
+    assert pending == ("********** Private Information **********\nPrivate info pending...\n"
+                       "***************************\n")
+    for c in HAND_GAME["chance"]:
+        o.apply_action(c)
+    for k, mv in enumerate(HAND_GAME["moves"][:HAND_TEXT_AFTER + 1]):
+        o.apply_action(np.array([mv], np.int32))
+    book = o.market.to_string(0)
+    assert oracle_to_string(o, 0) == HAND_SETUP_TEXT + HAND_PUBLIC_TEXT + book
+    for p, priv in HAND_PRIVATE_TEXT.items():
+        assert oracle_information_state_string(o, p, 0) == (
+            "********** Private Information **********\n" + priv +
+            "******************************************\n\n" + HAND_PUBLIC_TEXT + book)
