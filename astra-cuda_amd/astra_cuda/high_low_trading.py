@@ -402,6 +402,9 @@ class HighLowTradingState:
         _check(self._lib.astra_high_low_observation(ctypes.byref(o), _raw_stream(g.device_id)))
         return player if ret else None
 
+    def fill_information_state_tensor(self, *args):  # :495-500: not implemented in the reference
+        _fatal("FillInformationStateTensor not implemented")
+
     def expose_info(self) -> dict:  # :475-485
         if not self.is_terminal():
             _fatal("ExposeInfo called on non-terminal state")
