@@ -50,7 +50,7 @@ PROTOTYPES = {
 class HLTrade(ctypes.Structure):
     """astra_hl_trade (include/astra_high_low.h)."""
     _fields_ = [(n, _vp) for n in (
-        "move", "columns", "player_last_positions", "target_positions", "contract_values",
+        "move", "player_last_positions", "target_positions", "contract_values",
         "player_contract_over_time", "market_contract_over_time", "immediate_rewards",
         "rewards_since_last_action", "fill_prices", "fill_sizes", "fill_customer_ids",
         "fill_quoter_ids", "fill_is_sell_quote", "fill_quote_sizes", "fill_tid", "fill_quote_tid",

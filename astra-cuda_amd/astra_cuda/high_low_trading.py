@@ -8,8 +8,9 @@ One state holds ``num_markets`` independent envs, each a VecMarket market.
 
 The trading move (ApplyPlayerTrading, high_low_trading.cc:247-329) and
 FillObservationTensor (:510-602) run as the HIP kernels of
-include/astra_high_low.h: three launches per move and one sync for the input
-checks (the reference makes eight); ``check_moves=False`` drops that sync, and
+include/astra_high_low.h: one launch of the matching kernel with the game's
+work fused, plus a check launch and one sync for the input checks (the
+reference makes eight); ``check_moves=False`` drops the check and the sync, and
 ``check_errors()`` then reports any move that failed a check. The chance moves
 (:136-226), rewards, returns and reset are the reference's tensor operations.
 """
@@ -155,7 +156,6 @@ class HighLowTradingState:
             self.bbo_batch = o.bbo_batch.clone()
             self.fill_batch = o.fill_batch.clone()
             self._move_number = o._move_number
-        self._columns = torch.empty((5, N), dtype=torch.int32, device=self._dev)
         self._errors = torch.zeros((1,), dtype=torch.int32, device=self._dev)
         self._lib = _native.lib()
         self._trade = self._make_trade_args()
@@ -165,7 +165,7 @@ class HighLowTradingState:
         t = _native.HLTrade()
         fb, bb = self.fill_batch, self.bbo_batch
         ptrs = {
-            "columns": self._columns, "player_last_positions": self.player_last_positions,
+            "player_last_positions": self.player_last_positions,
             "target_positions": self.target_positions, "contract_values": self.contract_values,
             "player_contract_over_time": self.player_contract_over_time,
             "market_contract_over_time": self.market_contract_over_time,

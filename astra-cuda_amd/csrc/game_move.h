@@ -1,0 +1,132 @@
+// game_move.h -- the high-low game's trading move fused into the matching
+// kernel (nlyu1/astra-cuda src/games/high_low_trading/high_low_trading.cc:247-329).
+//
+// One lane per env does, around its market's matching: before it, the range
+// checks of the move (:264-271; a bit per failed check is OR-ed into *errors)
+// and the snapshot of the players' portfolios (CopyCustomerPortfoliosTo, :257);
+// after it, GetBBOs and UpdateLastPrices (:279-280), the telemetry rows
+// (:284-288) and every player's immediate reward and reward since last action
+// (:277, :290-328) in int32 with wrap-around, as libtorch's int32 kernels do.
+// The matching kernel's own inputs come from the move row (:260-263) and the
+// acting player (the customer id, :264).
+#pragma once
+
+#include <cstdint>
+
+struct astra_market;
+
+struct GameMove {
+  const int32_t *move;          // [M,4]: bid_px, ask_px, bid_sz, ask_sz
+  int32_t *last_pos;            // [M,P,2]
+  const int32_t *target;        // [M,P]
+  const int32_t *contract_values;  // [M,3]
+  int32_t *pcot;                // [M,P,T,6]
+  int32_t *mcot;                // [M,P*T,3]
+  int32_t *imm, *rsla;          // [M,P]
+  int32_t *bbo_out[4];          // best bid px, bid size, ask px, ask size [M]
+  int32_t *last_prices;         // [M]
+  int32_t *errors;              // [1]
+  int32_t P, T, S, V, player, tmn;
+};
+
+// The move's four values and the range-check bits (high_low_trading.cc:264-271).
+struct GameQuote {
+  int32_t bid_px, ask_px, bid_sz, ask_sz, bad;
+};
+
+ASTRA_HD GameQuote game_quote(const GameMove &g, int64_t m) {
+  GameQuote q;
+  q.bid_px = g.move[m * 4 + 0];
+  q.ask_px = g.move[m * 4 + 1];
+  q.bid_sz = g.move[m * 4 + 2];
+  q.ask_sz = g.move[m * 4 + 3];
+  q.bad = (!(q.bid_px > 0) ? 1 : 0) | (!(q.ask_px > 0) ? 2 : 0) | (!(q.bid_px <= g.V) ? 4 : 0) |
+          (!(q.ask_px <= g.V) ? 8 : 0) | (!(q.bid_sz >= 0) ? 16 : 0) | (!(q.ask_sz >= 0) ? 32 : 0) |
+          (!(q.bid_sz <= g.S) ? 64 : 0) | (!(q.ask_sz <= g.S) ? 128 : 0);
+  return q;
+}
+
+ASTRA_HD int32_t g_add(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+ASTRA_HD int32_t g_sub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
+ASTRA_HD int32_t g_mul(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
+ASTRA_HD int32_t g_abs(int32_t a) { return a < 0 ? (int32_t)(0u - (uint32_t)a) : a; }
+
+// Loads a portfolio word past the L1 cache: the lane's own fire-and-forget
+// atomics updated it at L2 after an earlier read may have cached it in L1.
+ASTRA_HD int32_t load_past_l1(const int32_t *p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  return *p;
+#endif
+}
+
+// Before the matching: checks and the portfolio snapshot of env m.
+ASTRA_HD void game_before(const GameMove &g, const int32_t *pf_m, int64_t m, int32_t bad) {
+  if (bad) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    atomicOr(g.errors, bad);
+#else
+    *g.errors |= bad;
+#endif
+  }
+  for (int32_t p = 0; p < g.P; ++p) {
+    g.last_pos[(m * g.P + p) * 2] = pf_m[p * 2];
+    g.last_pos[(m * g.P + p) * 2 + 1] = pf_m[p * 2 + 1];
+  }
+}
+
+// After the matching (its fill rows and portfolio atomics issued): BBO, last
+// price, telemetry and rewards of env m. fills = this call's fill count,
+// last_px = the price of its last fill row.
+ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *pf_m, int64_t m,
+                         const int32_t (&bbo)[4], int32_t fills, int32_t last_px) {
+  for (int k = 0; k < 4; ++k) g.bbo_out[k][m] = bbo[k];
+  int32_t last = g.last_prices[m];
+  if (fills > 0) {  // UpdateLastPrices (market.cu:767-786)
+    last = last_px;
+    g.last_prices[m] = last;
+  }
+  const int32_t P = g.P, T = g.T, V = g.V, player = g.player, tmn = g.tmn, pmn = tmn / P;
+  int32_t *pc = g.pcot + m * P * (int64_t)T * 6;
+  int32_t *mine = pc + ((int64_t)player * T + pmn) * 6;
+  mine[0] = q.bid_px;
+  mine[1] = q.ask_px;
+  mine[2] = q.bid_sz;
+  mine[3] = q.ask_sz;
+  int32_t *mc = g.mcot + (m * (int64_t)P * T + tmn) * 3;
+  mc[0] = bbo[0];
+  mc[1] = bbo[2];
+  mc[2] = last;
+  const int32_t mn = q.bid_sz < q.ask_sz ? q.bid_sz : q.ask_sz;
+  const int32_t cross = g_add(g_sub(q.bid_px, q.ask_px), 1);
+  const int32_t penalty = g_mul(g_mul(g_add(mn, 1), cross > 0 ? cross : 0), V);  // :308
+  const int32_t bid_cheap = (q.bid_sz == 0 && q.bid_px != 1) ? V : 0;          // :314
+  const int32_t ask_cheap = (q.ask_sz == 0 && q.ask_px != V) ? V : 0;          // :315
+  const bool settle = tmn == T * P - 1;                                         // :319
+  const int32_t value = g.contract_values[m * 3 + 2];
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_s_waitcnt(0);  // this lane's portfolio atomics have reached L2
+#endif
+  for (int32_t p = 0; p < P; ++p) {
+    const int32_t c_con = load_past_l1(pf_m + p * 2), c_cash = load_past_l1(pf_m + p * 2 + 1);
+    const int32_t l_con = g.last_pos[(m * P + p) * 2], l_cash = g.last_pos[(m * P + p) * 2 + 1];
+    const int32_t tgt = g.target[m * P + p];
+    pc[((int64_t)p * T + pmn) * 6 + 4] = c_con;
+    pc[((int64_t)p * T + pmn) * 6 + 5] = c_cash;
+    int32_t r = tgt != 0 ? g_mul(g_sub(g_abs(g_sub(l_con, tgt)), g_abs(g_sub(c_con, tgt))), V) : 0;
+    r = g_add(r, g_sub(c_cash, l_cash));
+    if (p == player) r = g_sub(g_sub(g_sub(r, penalty), bid_cheap), ask_cheap);
+    if (settle) r = g_add(r, g_mul(c_con, value));
+    g.imm[m * P + p] = r;
+    const int32_t before = p == player ? 0 : g.rsla[m * P + p];  // :277
+    g.rsla[m * P + p] = g_add(before, r);
+  }
+}
+
+// One fused trading move of every env of `market` (implemented with the matching
+// kernel in market.hip): the fills go to the [M,F,8] rows when `fill_rows` is set,
+// else to the eight field arrays; advances the TID counter by 2 like
+// astra_market_add_two_sided_quotes.
+int astra_game_move(astra_market *market, const GameMove &g, int32_t *const fill_fields[8],
+                    int32_t *fill_rows, int32_t *fill_counts, hipStream_t stream);

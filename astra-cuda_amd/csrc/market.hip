@@ -48,6 +48,7 @@
 
 #define ASTRA_SRC_NAME "market.hip"
 #include "runtime.h"
+#include "game_move.h"
 
 using namespace astra_rt;
 
@@ -143,9 +144,12 @@ Book book_of(const astra_market *h) {
   return b;
 }
 
+// The call's quotes: five [M] columns, or (the game's trading move) the [M,4]
+// move rows and the acting player in `game`.
 struct QuoteIn {
   const int32_t *bid_px, *bid_sz, *ask_px, *ask_sz, *cust;
   int32_t base_tid;
+  GameMove game;
 };
 
 // Fill rows go either to the reference's eight [M,F] arrays or, when `rows` is
@@ -430,6 +434,7 @@ struct MarketCtx {
   int32_t *pf;
   int32_t ns;             // ring position after the inserts
   bool bid_ok, ask_ok;
+  GameQuote gq;           // the game's move (GAME only)
 };
 
 // The matching loop's state: everything a lane needs to resume the loop later.
@@ -444,6 +449,7 @@ struct LoopState {
   uint32_t pbw, paw;
   bool ahead;                  // read-ahead issued for the current levels
   int32_t fc;                  // fills so far (-1 after an overflow)
+  int32_t last_px;             // price of the last fill row written
   uint32_t emptied, forwarded; // diagnostic counts
 };
 
@@ -494,7 +500,7 @@ struct StagedBook {
 // all at once, before the inserts write anything; the values are then patched
 // for what the inserts wrote (a slot the ring reuses, a tail link), so the
 // first loop pass starts with everything in registers.
-template <int W>
+template <int W, bool GAME>
 ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, MarketCtx &c,
                              LoopState<W> &s) {
   const int64_t M = b.M;
@@ -511,9 +517,22 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   uint4 *rec = c.rec;
 
   // ---- round trip 1 ----
-  const int32_t bid_px = in.bid_px[m], bid_sz = in.bid_sz[m];
-  const int32_t ask_px = in.ask_px[m], ask_sz = in.ask_sz[m];
-  const int32_t cust = in.cust[m];
+  int32_t bid_px, bid_sz, ask_px, ask_sz, cust;
+  if (GAME) {
+    c.gq = game_quote(in.game, m);
+    bid_px = c.gq.bid_px;
+    bid_sz = c.gq.bid_sz;
+    ask_px = c.gq.ask_px;
+    ask_sz = c.gq.ask_sz;
+    cust = in.game.player;
+    game_before(in.game, c.pf, m, c.gq.bad);
+  } else {
+    bid_px = in.bid_px[m];
+    bid_sz = in.bid_sz[m];
+    ask_px = in.ask_px[m];
+    ask_sz = in.ask_sz[m];
+    cust = in.cust[m];
+  }
 #pragma unroll
   for (int i = 0; i < W; ++i) {
     s.bm[i] = b.masks[(int64_t)i * M + m];
@@ -639,6 +658,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   s.paw = paw;
   s.ahead = cross;
   s.fc = 0;
+  s.last_px = 0;
   s.emptied = s.forwarded = 0;
 }
 
@@ -676,6 +696,7 @@ ASTRA_HD bool zero_walk(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, 
     int32_t row[8];
     make_row(s.brec, s.arec, 0, row);
     sink.put(out, c.pf, c.C, row);
+    s.last_px = row[0];
     ++s.fc;
     h = nh;
     w = bk.record(nh);
@@ -766,6 +787,7 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
       break;
     }
     sink.put(out, c.pf, c.C, row);  // the row and its portfolio update (:198-232)
+    s.last_px = row[0];
     ++s.fc;
     // (:237-238) both decrements land on one slot when bid and ask alias
     if (s.bh == s.ah) {
@@ -834,9 +856,10 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
 // position, and the best bid/offer of the book as left (what get_bbo_kernel,
 // market.cu:280-320, would read) into the workspace's BBO cache. STATS also
 // adds the call's work counts.
-template <int W, bool STATS, class BookMem>
+template <int W, bool STATS, bool GAME, class BookMem>
 ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx &c,
-                             const LoopState<W> &s, FillSink &sink, const BookMem &bk) {
+                             const LoopState<W> &s, FillSink &sink, const BookMem &bk,
+                             const GameMove &game) {
   const int64_t M = b.M, m = c.m;
   const int32_t L = c.L, O = c.O;
   // Loads first, then plain stores and the fill rows with their portfolio
@@ -853,11 +876,17 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
   }
   b.next_slot[m] = c.ns;
   sink.flush(out, c.pf, c.C);  // overlaps the loads above
-  b.bbo[m] = (s.bb >= 0 && s.bh < (uint32_t)O) ? s.bb : ASTRA_NULL_INDEX;
+  const int32_t obp = (s.bb >= 0 && s.bh < (uint32_t)O) ? s.bb : ASTRA_NULL_INDEX;
+  const int32_t oap = (s.ba < L && s.ah < (uint32_t)O) ? s.ba : ASTRA_NULL_INDEX;
+  b.bbo[m] = obp;
   b.bbo[M + m] = obs;
-  b.bbo[2 * M + m] = (s.ba < L && s.ah < (uint32_t)O) ? s.ba : ASTRA_NULL_INDEX;
+  b.bbo[2 * M + m] = oap;
   b.bbo[3 * M + m] = oas;
   b.tob[m] = ((s.bb >= 0 ? s.bh : kNull16) & kNull16) | ((s.ba < L ? s.ah : kNull16) << 16);
+  if (GAME) {
+    const int32_t bbo[4] = {obp, obs, oap, oas};
+    game_after(game, c.gq, c.pf, m, bbo, s.fc, s.last_px);
+  }
 
   if (STATS) {  // uniform addresses: the compiler aggregates these per wave
     add_u64(b.stats + 0, (unsigned long long)(c.bid_ok + c.ask_ok));
@@ -976,7 +1005,7 @@ ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
 //      the market's order records and level words into LDS with coalesced
 //      loads, and the owning lane resumes its loop reading from LDS.
 // All 64 lanes of a wavefront reach the ballots (no early return).
-template <int W, bool STATS>
+template <int W, bool STATS, bool GAME>
 __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, FillOut out,
                                                           int32_t budget, int32_t wave_words) {
   extern __shared__ int32_t lds_words[];
@@ -994,11 +1023,11 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
   LoopState<W> st;
   bool suspended = false;
   if (m < b.M) {
-    quote_prologue<W>(b, in, m, c, st);
+    quote_prologue<W, GAME>(b, in, m, c, st);
     sink.base = m * (int64_t)b.F;
     const GlobalBook gb{c.lv, c.rec};
     if (match_loop<W, STATS>(st, c, gb, sink, out, bulk, budget)) {
-      quote_epilogue<W, STATS>(b, out, c, st, sink, gb);
+      quote_epilogue<W, STATS, GAME>(b, out, c, st, sink, gb, in.game);
     } else {
       sink.flush(out, c.pf, c.C);  // frees the LDS for staging
       suspended = true;
@@ -1064,7 +1093,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     for (int32_t j = lane; j < b.L; j += 64) glv[j] = slv[j];
     if (lane == src) {
       sink.base = rb.base;
-      quote_epilogue<W, STATS>(b, out, c, st, sink, sb);
+      quote_epilogue<W, STATS, GAME>(b, out, c, st, sink, sb, in.game);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1109,7 +1138,7 @@ __global__ __launch_bounds__(kFillThreads) void fill_u32_kernel(uint32_t *dst, i
 
 inline unsigned grid_for(int64_t n, int block) { return (unsigned)((n + block - 1) / block); }
 
-template <int W>
+template <int W, bool GAME>
 int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &fo,
                        hipStream_t s) {
   const Book b = book_of(h);
@@ -1129,14 +1158,14 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
     FillSink sink;
     MarketCtx c;
     LoopState<W> st;
-    quote_prologue<W>(b, in, m, c, st);
+    quote_prologue<W, GAME>(b, in, m, c, st);
     sink.base = m * (int64_t)b.F;
     const GlobalBook gb{c.lv, c.rec};
     const bool done = b.stats ? match_loop<W, true>(st, c, gb, sink, fo, bulk, budget)
                               : match_loop<W, false>(st, c, gb, sink, fo, bulk, budget);
     if (done) {
-      if (b.stats) quote_epilogue<W, true>(b, fo, c, st, sink, gb);
-      else quote_epilogue<W, false>(b, fo, c, st, sink, gb);
+      if (b.stats) quote_epilogue<W, true, GAME>(b, fo, c, st, sink, gb, in.game);
+      else quote_epilogue<W, false, GAME>(b, fo, c, st, sink, gb, in.game);
     } else {  // the second pass, as on the GPU
       sink.flush(fo, c.pf, c.C);
       std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
@@ -1154,8 +1183,8 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
       std::memcpy(c.rec, srec.data(), (size_t)h->O * 16);
       std::memcpy(c.lv, slv.data(), (size_t)h->L * 8);
       sink.base = rb.base;
-      if (b.stats) quote_epilogue<W, true>(b, fo, c, st, sink, sb);
-      else quote_epilogue<W, false>(b, fo, c, st, sink, sb);
+      if (b.stats) quote_epilogue<W, true, GAME>(b, fo, c, st, sink, sb, in.game);
+      else quote_epilogue<W, false, GAME>(b, fo, c, st, sink, sb, in.game);
     }
     if (bulk.count > 0) write_bulk_host(fo, bulk);
   }
@@ -1165,10 +1194,10 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   const size_t lds = (size_t)(h->block / 64) * wave_bytes;
   const int32_t wave_words = (int32_t)(wave_bytes / 4);
   if (b.stats)
-    hipLaunchKernelGGL((quote_match_kernel<W, true>), dim3(grid_for(b.M, h->block)),
+    hipLaunchKernelGGL((quote_match_kernel<W, true, GAME>), dim3(grid_for(b.M, h->block)),
                        dim3(h->block), lds, s, b, in, fo, budget, wave_words);
   else
-    hipLaunchKernelGGL((quote_match_kernel<W, false>), dim3(grid_for(b.M, h->block)),
+    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME>), dim3(grid_for(b.M, h->block)),
                        dim3(h->block), lds, s, b, in, fo, budget, wave_words);
 #endif
   ASTRA_HIP_CHECK(rt_last_error(), "AddTwoSidedQuotes");
@@ -1201,6 +1230,18 @@ int launch_clear_quotes(const astra_market *h, const uint8_t *reset, hipStream_t
 #endif
   ASTRA_HIP_CHECK(rt_last_error(), "ClearQuotes");
   return ASTRA_OK;
+}
+
+template <int W>
+int launch_quote_match_plain(const astra_market *h, const QuoteIn &in, const FillOut &fo,
+                             hipStream_t s) {
+  return launch_quote_match<W, false>(h, in, fo, s);
+}
+
+template <int W>
+int launch_quote_match_game(const astra_market *h, const QuoteIn &in, const FillOut &fo,
+                            hipStream_t s) {
+  return launch_quote_match<W, true>(h, in, fo, s);
 }
 
 #define ASTRA_DISPATCH_W(W_, FN, ...)  \
@@ -1428,7 +1469,7 @@ int astra_market_add_two_sided_quotes(astra_market *h, const int32_t *bid_px,
                      fill_is_sell_quote, fill_quote_sizes, fill_tid,          fill_quote_tid,
                      fill_counts,        nullptr};
     const int rc = [&]() -> int {
-      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match, h, in, fo, as_stream(stream));
+      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_plain, h, in, fo, as_stream(stream));
     }();
     if (rc) return rc;
   }
@@ -1454,13 +1495,46 @@ int astra_market_add_two_sided_quotes_rows(astra_market *h, const int32_t *bid_p
     fo.counts = fill_counts;
     fo.rows = fill_rows;
     const int rc = [&]() -> int {
-      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match, h, in, fo, as_stream(stream));
+      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_plain, h, in, fo, as_stream(stream));
     }();
     if (rc) return rc;
   }
   h->tid = (int32_t)((uint32_t)h->tid + 2u);  // market.cu:531
   return ASTRA_OK;
 }
+
+}  // extern "C"
+
+int astra_game_move(astra_market *h, const GameMove &g, int32_t *const fill_fields[8],
+                    int32_t *fill_rows, int32_t *fill_counts, hipStream_t stream) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  if (h->M > 0) {
+    DeviceGuard dg(h->device);
+    QuoteIn in{nullptr, nullptr, nullptr, nullptr, nullptr, h->tid, g};
+    FillOut fo{};
+    fo.counts = fill_counts;
+    if (fill_rows) {
+      fo.rows = fill_rows;
+    } else {
+      fo.prices = fill_fields[0];
+      fo.sizes = fill_fields[1];
+      fo.taker = fill_fields[2];
+      fo.quoter = fill_fields[3];
+      fo.is_sell_quote = reinterpret_cast<uint8_t *>(fill_fields[4]);
+      fo.quote_sizes = fill_fields[5];
+      fo.tid = fill_fields[6];
+      fo.quote_tid = fill_fields[7];
+    }
+    const int rc = [&]() -> int {
+      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_game, h, in, fo, stream);
+    }();
+    if (rc) return rc;
+  }
+  h->tid = (int32_t)((uint32_t)h->tid + 2u);  // market.cu:531
+  return ASTRA_OK;
+}
+
+extern "C" {
 
 int astra_market_get_bbos(const astra_market *h, int32_t *bid_px, int32_t *bid_sz,
                           int32_t *ask_px, int32_t *ask_sz, void *stream) {

@@ -337,7 +337,7 @@ def bench_game(args):
         torch.cuda.synchronize()
         lat.append(time.perf_counter() - h0)
     lat_ms = np.array(lat) * 1e3
-    # C: device time per move (three kernels), unchecked moves back to back
+    # C: device time per move (one fused launch), unchecked moves back to back
     st = snaps[2]
     st.set_check_moves(False)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
@@ -359,11 +359,12 @@ def bench_game(args):
     st.market._set_stats(None)
     n_ins, n_fill, n_empty = (int(x) for x in counters.cpu().tolist()[:3])
     # algorithmic bytes per move: the matching kernel's (24 B per env + 32 per insert +
-    # 109 per fill row + 8 per emptied level) plus the move kernels': move 16 B, input
-    # columns 20 B and a 16*P B portfolio snapshot before; BBO 32 B, fill count and
-    # last price 8 B, move 16 B, telemetry 28 + 8*P B, and per player portfolio and
-    # snapshot 16 B, target 4 B, rewards 12 B after, plus the contract value 4 B.
-    game_bytes = N * ((16 + 20 + 16 * P) + (32 + 8 + 16 + 28 + 8 * P + 4 + 32 * P))
+    # 109 per fill row + 8 per emptied level) plus the game's work fused into it:
+    # reads of the move 16 B, contract value 4 B, last price 4 B and per player the
+    # portfolio 8 B, target 4 B and reward since last action 4 B; writes of the BBO
+    # 16 B, last price 4 B, telemetry 28 B and per player the portfolio snapshot
+    # 8 B, telemetry 8 B, immediate reward 4 B and reward since last action 4 B.
+    game_bytes = N * ((16 + 4 + 4 + 16 * P) + (16 + 4 + 28 + 24 * P))
     step_bytes = (24.0 * N * K + 32.0 * n_ins + 109.0 * n_fill + 8.0 * n_empty) / K + game_bytes
     achieved = step_bytes / (step_ms * 1e-3) / 1e9
     result = {
@@ -391,10 +392,10 @@ def bench_game(args):
         "ms_per_step_unchecked": wall_unchecked / K * 1e3,
         "p50_step_latency_ms": float(np.percentile(lat_ms, 50)),
         "p99_step_latency_ms": float(np.percentile(lat_ms, 99)),
-        "device_ms_per_step": {"move_kernels": step_ms},
+        "device_ms_per_step": {"fused_move_kernel": step_ms},
         "work_per_step": {"inserts": n_ins / K, "fill_rows": n_fill / K, "levels_emptied": n_empty / K},
         "roofline": {
-            "kernel": "trade_pre + quote_match + trade_post", "bound": "hbm",
+            "kernel": "quote_match_kernel with the game move fused (one launch per move)", "bound": "hbm",
             "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
             "traffic": None, "algorithmic_bytes_per_launch": step_bytes,
         },

@@ -8,8 +8,10 @@
  * HighLowTradingState::FillObservationTensor (:510-602). The reference runs each
  * trading move as about forty libtorch kernels plus eight .item() host syncs for
  * its input checks and a host-to-device copy of the customer ids; here a move is
- * three launches (checks and snapshot, the matching kernel, rewards and
- * telemetry) with at most one host sync, and an observation is one launch.
+ * one launch of the matching kernel with the game's checks, portfolio snapshot,
+ * BBO, last price, telemetry and rewards fused around each env's matching (plus,
+ * with check = 1, a check launch and one host sync before it), and an
+ * observation is one launch.
  *
  * All pointers are device pointers to int32 (uint8 for the bool settle flags,
  * float for observations), row-major and contiguous; the caller owns them.
@@ -40,7 +42,6 @@ extern "C" {
 /* One trading move of every env (the state tensors of high_low_trading.h:85-115). */
 typedef struct astra_hl_trade {
   const int32_t *move;            /* [N,4]: bid_px, ask_px, bid_sz, ask_sz (:260-263) */
-  int32_t *columns;               /* [5,N] scratch: the four move columns and the customer ids */
   int32_t *player_last_positions; /* [N,P,2] */
   const int32_t *target_positions;/* [N,P] */
   const int32_t *contract_values; /* [N,3] */

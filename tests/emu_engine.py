@@ -256,7 +256,6 @@ class EmuHighLow:
         self.market_contract_over_time = z(N, P * T, 3)
         self.immediate_rewards = z(N, P)
         self.rewards_since_last_action = z(N, P)
-        self.columns = z(5, N)
         self.errors = z(1)
         self._HLTrade, self._HLObservation = HLTrade, HLObservation
 
@@ -264,7 +263,7 @@ class EmuHighLow:
         self.move = np.ascontiguousarray(move, np.int32)
         t = self._HLTrade()
         ptr = lambda a: a.ctypes.data  # noqa: E731
-        for name in ("columns", "player_last_positions", "target_positions", "contract_values",
+        for name in ("player_last_positions", "target_positions", "contract_values",
                      "player_contract_over_time", "market_contract_over_time", "immediate_rewards",
                      "rewards_since_last_action", "errors"):
             setattr(t, name, ptr(getattr(self, name)))
