@@ -31,6 +31,7 @@ PROTOTYPES = {
     "astra_update_last_prices": (_c_int, [_vp, _vp, _vp, _c_i32, _c_i32, _vp]),
     "astra_market_add_two_sided_quotes_rows": (_c_int, [_vp] + [_vp] * 5 + [_vp, _vp, _vp]),
     "astra_update_last_prices_rows": (_c_int, [_vp, _vp, _vp, _c_i32, _c_i32, _vp]),
+    "astra_market_add_two_sided_quotes_steps": (_c_int, [_vp, _c_i32] + [_vp] * 5 + [_vp] * 12 + [_vp]),
     "astra_fill_i32": (_c_int, [_vp, ctypes.c_int64, _c_i32, _vp]),
     "astra_market_reset": (_c_int, [_vp, _vp]),
     "astra_market_clear_quotes": (_c_int, [_vp, _vp, _vp]),

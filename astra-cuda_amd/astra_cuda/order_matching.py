@@ -412,6 +412,51 @@ class VecMarket:
 
     AddTwoSidedQuotes = add_two_sided_quotes
 
+    def add_two_sided_quotes_steps(self, bid_px, bid_sz, ask_px, ask_sz, customer_ids, fills,
+                                   step_fill_counts=None, step_bbos=None) -> None:
+        """``steps`` consecutive add_two_sided_quotes calls in one launch (not in the
+        reference): the inputs are int32 ``[steps, M]`` tensors, row k being step k's
+        quotes. Afterwards the engine, ``fills`` and the BBOs that get_bbos reads are
+        exactly as after the single calls. ``step_fill_counts`` (int32 ``[steps, M]``)
+        receives every step's fill counts and ``step_bbos`` (int32 ``[4, steps, M]``:
+        best bid price, bid size, ask price, ask size) every step's get_bbos.
+        Asynchronous."""
+        M = self._M
+        names = ("bid_px", "bid_sz", "ask_px", "ask_sz", "customer_ids")
+        ts = (bid_px, bid_sz, ask_px, ask_sz, customer_ids)
+        if bid_px.dim() != 2:
+            _fatal("order_matching.py bid_px must be [steps, num_markets]")
+        steps = bid_px.size(0)
+        dev = self._device
+        for name, t in zip(names, ts):
+            if tuple(t.shape) != (steps, M):
+                _fatal(f"order_matching.py {name} must be [{steps}, {M}], got {list(t.shape)}")
+            if t.device != dev:
+                _fatal(f"{name} tensor must be on device {self._device_index}")
+            if not t.is_contiguous():
+                _fatal(f"{name} tensor must be contiguous")
+            if t.dtype != torch.int32:
+                _fatal(f"{name} tensor must be int32, got {t.dtype}")
+        for name, t, shape in (("step_fill_counts", step_fill_counts, (steps, M)),
+                               ("step_bbos", step_bbos, (4, steps, M))):
+            if t is None:
+                continue
+            if tuple(t.shape) != shape or t.dtype != torch.int32 or not t.is_contiguous() \
+                    or t.device != dev:
+                _fatal(f"{name} must be a contiguous int32 tensor of shape {list(shape)} on device "
+                       f"{self._device_index}")
+        fp = fills._pointers(M, self._F, dev)
+        if fp[0] == "rows":
+            fields, rows, counts = (None,) * 8, fp[1], fp[2]
+        else:
+            fields, rows, counts = fp[:8], None, fp[8]
+        rc = self._lib.astra_market_add_two_sided_quotes_steps(
+            self._h, steps, *(t.data_ptr() for t in ts), *fields, rows, counts,
+            None if step_fill_counts is None else step_fill_counts.data_ptr(),
+            None if step_bbos is None else step_bbos.data_ptr(), _raw_stream(self._device_index))
+        if rc:
+            _fatal(_native.last_error())
+
     def get_bbos(self, bbos: BBOBatch) -> None:
         """GetBBOs (market.cu:573-597): best level and its head order's size per side,
         ``(NULL_INDEX, 0)`` for an empty side. Asynchronous."""

@@ -162,6 +162,32 @@ struct FillOut {
   int32_t *rows;
 };
 
+// Per-step outputs of a multi-step call (null when not wanted): every step's
+// fill counts ([steps, M]) and every step's GetBBOs ([4, steps, M]: bid price,
+// bid size, ask price, ask size). Inside the kernel the pointers are those of
+// the current step ([M] each, bbo[j] the j-th field).
+struct StepOut {
+  int32_t *counts;
+  int32_t *bbo[4];
+};
+
+// The quotes and per-step outputs of step k of a multi-step call: the [steps, M]
+// inputs at row k, TID base advanced by 2 per step (market.cu:531).
+ASTRA_HD void step_views(const QuoteIn &in, const StepOut &so, int64_t M, int32_t steps, int32_t k,
+                         QuoteIn &ink, StepOut &sok) {
+  const int64_t off = (int64_t)k * M;
+  ink = in;
+  ink.bid_px = in.bid_px + off;
+  ink.bid_sz = in.bid_sz + off;
+  ink.ask_px = in.ask_px + off;
+  ink.ask_sz = in.ask_sz + off;
+  ink.cust = in.cust + off;
+  ink.base_tid = (int32_t)((uint32_t)in.base_tid + 2u * (uint32_t)k);
+  sok.counts = so.counts ? so.counts + off : nullptr;
+  for (int j = 0; j < 4; ++j)
+    sok.bbo[j] = so.bbo[0] ? so.bbo[0] + ((int64_t)j * steps * M + off) : nullptr;
+}
+
 // ---- small device/host helpers ----
 
 ASTRA_HD int clz64(uint64_t x) {
@@ -856,10 +882,10 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
 // position, and the best bid/offer of the book as left (what get_bbo_kernel,
 // market.cu:280-320, would read) into the workspace's BBO cache. STATS also
 // adds the call's work counts.
-template <int W, bool STATS, bool GAME, class BookMem>
+template <int W, bool STATS, bool GAME, bool MULTI, class BookMem>
 ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx &c,
                              const LoopState<W> &s, FillSink &sink, const BookMem &bk,
-                             const GameMove &game) {
+                             const GameMove &game, const StepOut &so) {
   const int64_t M = b.M, m = c.m;
   const int32_t L = c.L, O = c.O;
   // Loads first, then plain stores and the fill rows with their portfolio
@@ -886,6 +912,15 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
   if (GAME) {
     const int32_t bbo[4] = {obp, obs, oap, oas};
     game_after(game, c.gq, c.pf, m, bbo, s.fc, s.last_px);
+  }
+  if (MULTI) {
+    if (so.counts) so.counts[m] = s.fc;
+    if (so.bbo[0]) {
+      so.bbo[0][m] = obp;
+      so.bbo[1][m] = obs;
+      so.bbo[2][m] = oap;
+      so.bbo[3][m] = oas;
+    }
   }
 
   if (STATS) {  // uniform addresses: the compiler aggregates these per wave
@@ -1004,102 +1039,116 @@ ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
 //      consumed orders) are finished one at a time: the whole wavefront copies
 //      the market's order records and level words into LDS with coalesced
 //      loads, and the owning lane resumes its loop reading from LDS.
+// MULTI runs `steps` consecutive calls in one launch: markets are independent,
+// so each wavefront goes on to its markets' next step as soon as it is done
+// with this one, with no grid-wide wait between steps.
 // All 64 lanes of a wavefront reach the ballots (no early return).
-template <int W, bool STATS, bool GAME>
+template <int W, bool STATS, bool GAME, bool MULTI>
 __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, FillOut out,
+                                                          StepOut so, int32_t steps,
                                                           int32_t budget, int32_t wave_words) {
   extern __shared__ int32_t lds_words[];
   const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int lane = (int)(threadIdx.x % 64);
   int32_t *wave_lds = lds_words + (threadIdx.x / 64) * wave_words;
-  Bulk bulk;
-  bulk.count = 0;
   FillSink sink;
 #if defined(__HIP_DEVICE_COMPILE__)
   sink.lds = wave_lds;
   sink.lane = lane;
 #endif
-  MarketCtx c;
-  LoopState<W> st;
-  bool suspended = false;
-  if (m < b.M) {
-    quote_prologue<W, GAME>(b, in, m, c, st);
-    sink.base = m * (int64_t)b.F;
-    const GlobalBook gb{c.lv, c.rec};
-    if (match_loop<W, STATS>(st, c, gb, sink, out, bulk, budget)) {
-      quote_epilogue<W, STATS, GAME>(b, out, c, st, sink, gb, in.game);
-    } else {
-      sink.flush(out, c.pf, c.C);  // frees the LDS for staging
-      suspended = true;
-    }
-  }
-  uint64_t todo = __ballot(suspended);
-  while (todo) {
-    const int src = __ffsll((unsigned long long)todo) - 1;
-    todo &= todo - 1;
-    const int64_t ms = shfl_i64(m, src);
-    uint4 *srec = reinterpret_cast<uint4 *>(wave_lds);
-    uint64_t *slv = reinterpret_cast<uint64_t *>(srec + b.O);
-    int32_t *rows = reinterpret_cast<int32_t *>(slv + b.L);
-    uint4 *grec = b.records + ms * (int64_t)b.O;
-    uint64_t *glv = reinterpret_cast<uint64_t *>(b.levels) + ms * (int64_t)b.L;
-    int32_t *pfm = b.portfolios + ms * (int64_t)b.C * 2;
-    __builtin_amdgcn_wave_barrier();
-#if defined(__HIP_DEVICE_COMPILE__)
-    // LDS DMA (global_load_lds): each lane's 16 (or 4) bytes go straight to
-    // LDS at the wave-uniform base + lane * size, no registers involved, all
-    // loads in flight together.
-    for (int32_t j = 0; j < b.O; j += 64)
-      if (j + lane < b.O)
-        __builtin_amdgcn_global_load_lds((gvoid_t *)(grec + j + lane), (lvoid_t *)(srec + j), 16, 0,
-                                         0);
-    const uint32_t *glv32 = reinterpret_cast<const uint32_t *>(glv);
-    uint32_t *slv32 = reinterpret_cast<uint32_t *>(slv);
-    for (int32_t j = 0; j < 2 * b.L; j += 64)
-      if (j + lane < 2 * b.L)
-        __builtin_amdgcn_global_load_lds((gvoid_t *)(glv32 + j + lane), (lvoid_t *)(slv32 + j), 4,
-                                         0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-#endif
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const StagedBook sb{reinterpret_cast<uint16_t *>(slv), srec};
-    RowBuffer rb{rows, kStageRows, 0, 0};
-    if (lane == src) rb.base = sink.base;
-    // The owning lane runs until its market is done or its row buffer is
-    // full; then all 64 lanes write the rows out, coalesced.
-    bool done = false;
-    while (!done) {
-      int32_t fin = 0;
-      if (lane == src) fin = match_loop<W, STATS>(st, c, sb, rb, out, bulk, 0x7FFFFFFF) ? 1 : 0;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int32_t n = __shfl(rb.n, src);
-      const int64_t base = shfl_i64(rb.base, src);
-      done = __shfl(fin, src) != 0;
-      flush_rows(out, rows, n, base, pfm, b.C, lane, 64);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (lane == src) {
-        rb.base += n;
-        rb.n = 0;
+  for (int32_t k = 0; k < (MULTI ? steps : 1); ++k) {
+    QuoteIn ink = in;
+    StepOut sok = so;
+    if (MULTI) step_views(in, so, b.M, steps, k, ink, sok);
+    Bulk bulk;
+    bulk.count = 0;
+    MarketCtx c;
+    LoopState<W> st;
+    bool suspended = false;
+    if (m < b.M) {
+      quote_prologue<W, GAME>(b, ink, m, c, st);
+      sink.base = m * (int64_t)b.F;
+      const GlobalBook gb{c.lv, c.rec};
+      if (match_loop<W, STATS>(st, c, gb, sink, out, bulk, budget)) {
+        quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, gb, ink.game, sok);
+      } else {
+        sink.flush(out, c.pf, c.C);  // frees the LDS for staging
+        suspended = true;
       }
     }
-    // the staged book back to global memory, coalesced
-    for (int32_t j = lane; j < b.O; j += 64) grec[j] = srec[j];
-    for (int32_t j = lane; j < b.L; j += 64) glv[j] = slv[j];
-    if (lane == src) {
-      sink.base = rb.base;
-      quote_epilogue<W, STATS, GAME>(b, out, c, st, sink, sb, in.game);
+    uint64_t todo = __ballot(suspended);
+    while (todo) {
+      const int src = __ffsll((unsigned long long)todo) - 1;
+      todo &= todo - 1;
+      const int64_t ms = shfl_i64(m, src);
+      uint4 *srec = reinterpret_cast<uint4 *>(wave_lds);
+      uint64_t *slv = reinterpret_cast<uint64_t *>(srec + b.O);
+      int32_t *rows = reinterpret_cast<int32_t *>(slv + b.L);
+      uint4 *grec = b.records + ms * (int64_t)b.O;
+      uint64_t *glv = reinterpret_cast<uint64_t *>(b.levels) + ms * (int64_t)b.L;
+      int32_t *pfm = b.portfolios + ms * (int64_t)b.C * 2;
+      __builtin_amdgcn_wave_barrier();
+#if defined(__HIP_DEVICE_COMPILE__)
+      // LDS DMA (global_load_lds): each lane's 16 (or 4) bytes go straight to
+      // LDS at the wave-uniform base + lane * size, no registers involved, all
+      // loads in flight together.
+      for (int32_t j = 0; j < b.O; j += 64)
+        if (j + lane < b.O)
+          __builtin_amdgcn_global_load_lds((gvoid_t *)(grec + j + lane), (lvoid_t *)(srec + j), 16,
+                                           0, 0);
+      const uint32_t *glv32 = reinterpret_cast<const uint32_t *>(glv);
+      uint32_t *slv32 = reinterpret_cast<uint32_t *>(slv);
+      for (int32_t j = 0; j < 2 * b.L; j += 64)
+        if (j + lane < 2 * b.L)
+          __builtin_amdgcn_global_load_lds((gvoid_t *)(glv32 + j + lane), (lvoid_t *)(slv32 + j), 4,
+                                           0, 0);
+      __builtin_amdgcn_s_waitcnt(0);
+#endif
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const StagedBook sb{reinterpret_cast<uint16_t *>(slv), srec};
+      RowBuffer rb{rows, kStageRows, 0, 0};
+      if (lane == src) rb.base = sink.base;
+      // The owning lane runs until its market is done or its row buffer is
+      // full; then all 64 lanes write the rows out, coalesced.
+      bool done = false;
+      while (!done) {
+        int32_t fin = 0;
+        if (lane == src) fin = match_loop<W, STATS>(st, c, sb, rb, out, bulk, 0x7FFFFFFF) ? 1 : 0;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int32_t n = __shfl(rb.n, src);
+        const int64_t base = shfl_i64(rb.base, src);
+        done = __shfl(fin, src) != 0;
+        flush_rows(out, rows, n, base, pfm, b.C, lane, 64);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane == src) {
+          rb.base += n;
+          rb.n = 0;
+        }
+      }
+      // the staged book back to global memory, coalesced
+      for (int32_t j = lane; j < b.O; j += 64) grec[j] = srec[j];
+      for (int32_t j = lane; j < b.L; j += 64) glv[j] = slv[j];
+      if (lane == src) {
+        sink.base = rb.base;
+        quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, sb, ink.game, sok);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    write_bulk_wave(out, bulk);
+    if (MULTI) {  // this step's rows and book writes come before the next step's
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
   }
-  write_bulk_wave(out, bulk);
 }
 
 __global__ __launch_bounds__(256) void bbo_kernel(Book b, int32_t *bid_px, int32_t *bid_sz,
@@ -1138,9 +1187,9 @@ __global__ __launch_bounds__(kFillThreads) void fill_u32_kernel(uint32_t *dst, i
 
 inline unsigned grid_for(int64_t n, int block) { return (unsigned)((n + block - 1) / block); }
 
-template <int W, bool GAME>
+template <int W, bool GAME, bool MULTI>
 int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &fo,
-                       hipStream_t s) {
+                       const StepOut &so, int32_t steps, hipStream_t s) {
   const Book b = book_of(h);
   // Staging needs the market's records and level words in LDS next to the
   // block's other wavefronts' buffers, within 64 KB per workgroup.
@@ -1152,41 +1201,46 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   std::vector<uint4> srec(staged ? (size_t)h->O : 0);
   std::vector<uint16_t> slv(staged ? (size_t)h->L * 4 : 0);
   std::vector<int32_t> rows((size_t)kStageRows * 8);
-  for (int64_t m = 0; m < b.M; ++m) {
-    Bulk bulk;
-    bulk.count = 0;
-    FillSink sink;
-    MarketCtx c;
-    LoopState<W> st;
-    quote_prologue<W, GAME>(b, in, m, c, st);
-    sink.base = m * (int64_t)b.F;
-    const GlobalBook gb{c.lv, c.rec};
-    const bool done = b.stats ? match_loop<W, true>(st, c, gb, sink, fo, bulk, budget)
-                              : match_loop<W, false>(st, c, gb, sink, fo, bulk, budget);
-    if (done) {
-      if (b.stats) quote_epilogue<W, true, GAME>(b, fo, c, st, sink, gb, in.game);
-      else quote_epilogue<W, false, GAME>(b, fo, c, st, sink, gb, in.game);
-    } else {  // the second pass, as on the GPU
-      sink.flush(fo, c.pf, c.C);
-      std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
-      std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
-      const StagedBook sb{slv.data(), srec.data()};
-      RowBuffer rb{rows.data(), kStageRows, 0, sink.base};
-      bool fin = false;
-      while (!fin) {
-        fin = b.stats ? match_loop<W, true>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF)
-                      : match_loop<W, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF);
-        flush_rows(fo, rows.data(), rb.n, rb.base, c.pf, c.C, 0, 1);
-        rb.base += rb.n;
-        rb.n = 0;
+  for (int32_t k = 0; k < (MULTI ? steps : 1); ++k) {
+    QuoteIn ink = in;
+    StepOut sok = so;
+    if (MULTI) step_views(in, so, b.M, steps, k, ink, sok);
+    for (int64_t m = 0; m < b.M; ++m) {
+      Bulk bulk;
+      bulk.count = 0;
+      FillSink sink;
+      MarketCtx c;
+      LoopState<W> st;
+      quote_prologue<W, GAME>(b, ink, m, c, st);
+      sink.base = m * (int64_t)b.F;
+      const GlobalBook gb{c.lv, c.rec};
+      const bool done = b.stats ? match_loop<W, true>(st, c, gb, sink, fo, bulk, budget)
+                                : match_loop<W, false>(st, c, gb, sink, fo, bulk, budget);
+      if (done) {
+        if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok);
+        else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok);
+      } else {  // the second pass, as on the GPU
+        sink.flush(fo, c.pf, c.C);
+        std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
+        std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
+        const StagedBook sb{slv.data(), srec.data()};
+        RowBuffer rb{rows.data(), kStageRows, 0, sink.base};
+        bool fin = false;
+        while (!fin) {
+          fin = b.stats ? match_loop<W, true>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF)
+                        : match_loop<W, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF);
+          flush_rows(fo, rows.data(), rb.n, rb.base, c.pf, c.C, 0, 1);
+          rb.base += rb.n;
+          rb.n = 0;
+        }
+        std::memcpy(c.rec, srec.data(), (size_t)h->O * 16);
+        std::memcpy(c.lv, slv.data(), (size_t)h->L * 8);
+        sink.base = rb.base;
+        if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok);
+        else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok);
       }
-      std::memcpy(c.rec, srec.data(), (size_t)h->O * 16);
-      std::memcpy(c.lv, slv.data(), (size_t)h->L * 8);
-      sink.base = rb.base;
-      if (b.stats) quote_epilogue<W, true, GAME>(b, fo, c, st, sink, sb, in.game);
-      else quote_epilogue<W, false, GAME>(b, fo, c, st, sink, sb, in.game);
+      if (bulk.count > 0) write_bulk_host(fo, bulk);
     }
-    if (bulk.count > 0) write_bulk_host(fo, bulk);
   }
 #else
   const size_t wave_bytes =
@@ -1194,11 +1248,11 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   const size_t lds = (size_t)(h->block / 64) * wave_bytes;
   const int32_t wave_words = (int32_t)(wave_bytes / 4);
   if (b.stats)
-    hipLaunchKernelGGL((quote_match_kernel<W, true, GAME>), dim3(grid_for(b.M, h->block)),
-                       dim3(h->block), lds, s, b, in, fo, budget, wave_words);
+    hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI>), dim3(grid_for(b.M, h->block)),
+                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words);
   else
-    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME>), dim3(grid_for(b.M, h->block)),
-                       dim3(h->block), lds, s, b, in, fo, budget, wave_words);
+    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI>), dim3(grid_for(b.M, h->block)),
+                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words);
 #endif
   ASTRA_HIP_CHECK(rt_last_error(), "AddTwoSidedQuotes");
   return ASTRA_OK;
@@ -1235,13 +1289,19 @@ int launch_clear_quotes(const astra_market *h, const uint8_t *reset, hipStream_t
 template <int W>
 int launch_quote_match_plain(const astra_market *h, const QuoteIn &in, const FillOut &fo,
                              hipStream_t s) {
-  return launch_quote_match<W, false>(h, in, fo, s);
+  return launch_quote_match<W, false, false>(h, in, fo, StepOut{}, 1, s);
 }
 
 template <int W>
 int launch_quote_match_game(const astra_market *h, const QuoteIn &in, const FillOut &fo,
                             hipStream_t s) {
-  return launch_quote_match<W, true>(h, in, fo, s);
+  return launch_quote_match<W, true, false>(h, in, fo, StepOut{}, 1, s);
+}
+
+template <int W>
+int launch_quote_match_steps(const astra_market *h, const QuoteIn &in, const FillOut &fo,
+                             const StepOut &so, int32_t steps, hipStream_t s) {
+  return launch_quote_match<W, false, true>(h, in, fo, so, steps, s);
 }
 
 #define ASTRA_DISPATCH_W(W_, FN, ...)  \
@@ -1503,6 +1563,51 @@ int astra_market_add_two_sided_quotes_rows(astra_market *h, const int32_t *bid_p
   return ASTRA_OK;
 }
 
+int astra_market_add_two_sided_quotes_steps(
+    astra_market *h, int32_t steps, const int32_t *bid_px, const int32_t *bid_sz,
+    const int32_t *ask_px, const int32_t *ask_sz, const int32_t *customer_ids,
+    int32_t *fill_prices, int32_t *fill_sizes, int32_t *fill_customer_ids, int32_t *fill_quoter_ids,
+    uint8_t *fill_is_sell_quote, int32_t *fill_quote_sizes, int32_t *fill_tid,
+    int32_t *fill_quote_tid, int32_t *fill_rows, int32_t *fill_counts, int32_t *step_fill_counts,
+    int32_t *step_bbos, void *stream) {
+  if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
+  if (steps < 0) return fail(ASTRA_ERR_INVALID_ARGUMENT, "steps must be >= 0");
+  if (steps == 0) return ASTRA_OK;
+  if (h->M > 0) {
+    if (!bid_px || !bid_sz || !ask_px || !ask_sz || !customer_ids || !fill_counts)
+      return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL input or fill_counts pointer");
+    if (fill_rows) {
+      if ((reinterpret_cast<uintptr_t>(fill_rows) & 15) != 0)
+        return fail(ASTRA_ERR_INVALID_ARGUMENT, "fill_rows must be 16-byte aligned");
+    } else if (h->F > 0 && (!fill_prices || !fill_sizes || !fill_customer_ids || !fill_quoter_ids ||
+                            !fill_is_sell_quote || !fill_quote_sizes || !fill_tid ||
+                            !fill_quote_tid)) {
+      return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL fill pointer");
+    }
+    DeviceGuard g(h->device);
+    const QuoteIn in{bid_px, bid_sz, ask_px, ask_sz, customer_ids, h->tid};
+    FillOut fo{};
+    fo.counts = fill_counts;
+    if (fill_rows) {
+      fo.rows = fill_rows;
+    } else {
+      fo = FillOut{fill_prices,        fill_sizes,       fill_customer_ids, fill_quoter_ids,
+                   fill_is_sell_quote, fill_quote_sizes, fill_tid,          fill_quote_tid,
+                   fill_counts,        nullptr};
+    }
+    StepOut so{};
+    so.counts = step_fill_counts;
+    so.bbo[0] = step_bbos;  // step_views derives the other three fields' rows
+    const int rc = [&]() -> int {
+      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_steps, h, in, fo, so, steps,
+                       as_stream(stream));
+    }();
+    if (rc) return rc;
+  }
+  h->tid = (int32_t)((uint32_t)h->tid + 2u * (uint32_t)steps);  // market.cu:531, per step
+  return ASTRA_OK;
+}
+
 }  // extern "C"
 
 int astra_game_move(astra_market *h, const GameMove &g, int32_t *const fill_fields[8],
@@ -1511,6 +1616,8 @@ int astra_game_move(astra_market *h, const GameMove &g, int32_t *const fill_fiel
   if (h->M > 0) {
     DeviceGuard dg(h->device);
     QuoteIn in{nullptr, nullptr, nullptr, nullptr, nullptr, h->tid, g};
+    if ((reinterpret_cast<uintptr_t>(fill_rows) & 15) != 0)
+      return fail(ASTRA_ERR_INVALID_ARGUMENT, "fill_rows must be 16-byte aligned");
     FillOut fo{};
     fo.counts = fill_counts;
     if (fill_rows) {

@@ -19,7 +19,10 @@ pre-timed state, so they see exactly the same work):
      emptied levels, for the algorithmic-byte roofline;
   R  the timed steps again with a FillBatch in the row layout
      (new_fill_batch(layout="rows"), not the reference's), reported beside the
-     headline as value_rows_layout.
+     headline as value_rows_layout;
+  S  the timed steps as ONE launch of the multi-step kernel
+     (add_two_sided_quotes_steps, not in the reference; every step's BBOs kept),
+     reported beside the headline under "multistep".
 Then the CPU baseline: the oracle (a C port of the reference algorithm) on a
 bounded subset of the same markets and steps, all host threads and 1 thread.
 
@@ -59,8 +62,9 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the all-thread oracle leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--phases", default="ABCDR",
-                    help="phases to run (A is always run; B latency, C events, D work counts)")
+    ap.add_argument("--phases", default="ABCDRS",
+                    help="phases to run (A is always run; B latency, C events, D work counts, "
+                         "R row layout, S multi-step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for rocprof counter scaling)")
     return ap.parse_args()
@@ -145,7 +149,7 @@ def main():
     torch.cuda.synchronize()
     phases = set(args.phases.upper()) | {"A"}
     # state at the start of the timed steps, for the replays B, C and D
-    snaps = [market.clone() if p in phases else None for p in "BCDR"]
+    snaps = [market.clone() if p in phases else None for p in "BCDRS"]
     torch.cuda.synchronize()
     log(f"warm-up done ({W} steps); timing {K} steps")
 
@@ -215,6 +219,25 @@ def main():
         torch.cuda.synchronize()
         wall_rows = time.perf_counter() - r0
         log(f"R: {K} steps in {wall_rows * 1e3:.2f} ms with the row layout")
+
+    # ---- S: the same K steps as ONE multi-step launch (every step's BBOs kept) ----
+    multistep = None
+    if "S" in phases:
+        sfills = snaps[4].new_fill_batch()
+        step_bbos = torch.empty((4, K, M), dtype=torch.int32, device=dev) if bbo else None
+        ins = [x[W:T] for x in dev_in]
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        s0 = time.perf_counter()
+        ev[0].record()
+        snaps[4].add_two_sided_quotes_steps(*ins, sfills, step_bbos=step_bbos)
+        ev[1].record()
+        torch.cuda.synchronize()
+        wall_ms = time.perf_counter() - s0
+        multistep = {"value": M * K / wall_ms, "ms_per_step": wall_ms / K * 1e3,
+                     "device_ms_per_step": ev[0].elapsed_time(ev[1]) / K, "steps_per_launch": K,
+                     "kernel": "quote_match_kernel (multi-step)"}
+        log(f"S: {K} steps in one launch, {wall_ms * 1e3:.2f} ms")
     log(f"work over {K} steps: inserts {n_ins}, fill rows {n_fill}, emptied {n_empty}, overflow {n_ovf}")
 
     # algorithmic bytes (per launch of the matching kernel): quotes in 20 B + fill_counts 4 B
@@ -247,6 +270,7 @@ def main():
         },
         "market_steps_per_s": K / wall,
         "value_rows_layout": (M * K / wall_rows) if wall_rows else None,
+        "multistep": multistep,
         "p50_step_latency_ms": float(np.percentile(lat_ms, 50)),
         "p99_step_latency_ms": float(np.percentile(lat_ms, 99)),
         "max_step_latency_ms": float(lat_ms.max()),

@@ -106,6 +106,28 @@ int astra_market_add_two_sided_quotes_rows(astra_market *market, const int32_t *
                                            int32_t *fill_rows, int32_t *fill_counts,
                                            void *stream);
 
+/* `steps` consecutive astra_market_add_two_sided_quotes calls in one launch.
+ * No counterpart in the reference: a caller with the quotes of several steps
+ * in hand (benchmarks, replays) runs them as one multi-step kernel in which each
+ * wavefront goes on to its markets' next step without a grid-wide wait between
+ * steps. The inputs are int32 [steps, M] arrays (row k = step k's quotes, TID
+ * base = the counter + 2k); the state afterwards (book, portfolios, TID counter,
+ * the fill batch, the BBO cache astra_market_get_bbos reads) is exactly that of
+ * the `steps` single calls, so the fill batch holds the last step's fills
+ * (rows beyond its count hold earlier steps' rows, as they would).
+ * fill_rows non-NULL selects the [M, F, 8] row layout of
+ * astra_market_add_two_sided_quotes_rows and the eight field pointers are not
+ * used. step_fill_counts (int32 [steps, M]) receives every step's fill_counts and
+ * step_bbos (int32 [4, steps, M]: best bid price, bid size, ask price, ask size)
+ * every step's GetBBOs; either may be NULL. steps = 0 does nothing. */
+int astra_market_add_two_sided_quotes_steps(
+    astra_market *market, int32_t steps, const int32_t *bid_px, const int32_t *bid_sz,
+    const int32_t *ask_px, const int32_t *ask_sz, const int32_t *customer_ids,
+    int32_t *fill_prices, int32_t *fill_sizes, int32_t *fill_customer_ids,
+    int32_t *fill_quoter_ids, uint8_t *fill_is_sell_quote, int32_t *fill_quote_sizes,
+    int32_t *fill_tid, int32_t *fill_quote_tid, int32_t *fill_rows, int32_t *fill_counts,
+    int32_t *step_fill_counts, int32_t *step_bbos, void *stream);
+
 /* VecMarket::GetBBOs (market.cu:573-597): four int32 [M] outputs. The values
  * are those of the book as the last mutating call left it (the matching kernel
  * computes them; this call copies them out). */

@@ -21,7 +21,8 @@ BUILD_DIR = os.path.join(HERE, "_build")
 EMU_LIB = os.path.join(BUILD_DIR, "libastra_market_emu.so")
 CSRC = os.path.join(ROOT, "astra-cuda_amd", "csrc")
 SRCS = [os.path.join(CSRC, f) for f in ("market.hip", "high_low.hip")]
-DEPS = SRCS + [os.path.join(CSRC, "runtime.h"), os.path.join(ROOT, "include", "astra_market.h"),
+DEPS = SRCS + [os.path.join(CSRC, "runtime.h"), os.path.join(CSRC, "game_move.h"),
+               os.path.join(ROOT, "include", "astra_market.h"),
                os.path.join(ROOT, "include", "astra_high_low.h")]
 
 _lib = None
@@ -149,6 +150,20 @@ class EmuMarket:
             return
         _check(lib().astra_market_add_two_sided_quotes(self.h, *[a.ctypes.data for a in ins],
                                                         *fills.ptrs(), None))
+
+    def add_two_sided_quotes_steps(self, bid_px, bid_sz, ask_px, ask_sz, cust, fills,
+                                   step_counts=None, step_bbos=None):
+        ins = [np.ascontiguousarray(a, np.int32) for a in (bid_px, bid_sz, ask_px, ask_sz, cust)]
+        steps = ins[0].shape[0]
+        if isinstance(fills, EmuRowFills):
+            fields, rows, counts = [None] * 8, fills.rows.ctypes.data, fills.fill_counts.ctypes.data
+        else:
+            p = fills.ptrs()
+            fields, rows, counts = p[:8], None, p[8]
+        _check(lib().astra_market_add_two_sided_quotes_steps(
+            self.h, steps, *[a.ctypes.data for a in ins], *fields, rows, counts,
+            None if step_counts is None else step_counts.ctypes.data,
+            None if step_bbos is None else step_bbos.ctypes.data, None))
 
     def get_bbos(self, b):
         _check(lib().astra_market_get_bbos(self.h, b.best_bid_prices.ctypes.data,
