@@ -56,7 +56,7 @@ class HLTrade(ctypes.Structure):
         "rewards_since_last_action", "fill_prices", "fill_sizes", "fill_customer_ids",
         "fill_quoter_ids", "fill_is_sell_quote", "fill_quote_sizes", "fill_tid", "fill_quote_tid",
         "fill_counts", "best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes",
-        "last_prices", "fill_rows", "errors")] + [(n, _c_i32) for n in (
+        "last_prices", "fill_rows", "errors", "errors_host")] + [(n, _c_i32) for n in (
         "players", "steps_per_player", "max_contracts_per_trade", "max_contract_value", "player",
         "trade_move_number", "check")]
 

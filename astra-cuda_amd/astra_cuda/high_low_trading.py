@@ -9,8 +9,10 @@ One state holds ``num_markets`` independent envs, each a VecMarket market.
 The trading move (ApplyPlayerTrading, high_low_trading.cc:247-329) and
 FillObservationTensor (:510-602) run as the HIP kernels of
 include/astra_high_low.h: one launch of the matching kernel with the game's
-work fused, plus a check launch and one sync for the input checks (the
-reference makes eight); ``check_moves=False`` drops the check and the sync, and
+work fused, plus a check launch and one host wait, for the checks only, while
+the move kernel runs (the reference makes eight syncs); a move that fails a
+check changes nothing and raises. ``check_moves=False`` drops the check and the
+wait, and
 ``check_errors()`` then reports any move that failed a check. The chance moves
 (:136-226), rewards, returns and reset are the reference's tensor operations.
 """
@@ -157,6 +159,8 @@ class HighLowTradingState:
             self.fill_batch = o.fill_batch.clone()
             self._move_number = o._move_number
         self._errors = torch.zeros((1,), dtype=torch.int32, device=self._dev)
+        # the checked move's error word lands here (pinned) for the one host wait
+        self._errors_host = torch.zeros((1,), dtype=torch.int32, pin_memory=True)
         self._lib = _native.lib()
         self._trade = self._make_trade_args()
 
@@ -185,6 +189,7 @@ class HighLowTradingState:
         for k, v in ptrs.items():
             assert v.is_contiguous() and v.device == self._dev, k
             setattr(t, k, v.data_ptr())
+        t.errors_host = self._errors_host.data_ptr()
         t.players, t.steps_per_player = self._P, self._T
         t.max_contracts_per_trade, t.max_contract_value = g.max_contracts_per_trade, g.max_contract_value
         t.check = 1 if g.check_moves else 0
@@ -325,7 +330,7 @@ class HighLowTradingState:
             _fatal(_native.last_error())
 
     def set_check_moves(self, check: bool) -> None:
-        """Switch the per-move input checks (one sync per move) on or off."""
+        """Switch the per-move input checks (one host wait per move) on or off."""
         self._trade.check = 1 if check else 0
 
     def check_errors(self) -> None:

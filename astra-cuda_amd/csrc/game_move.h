@@ -27,6 +27,8 @@ struct GameMove {
   int32_t *last_prices;         // [M]
   int32_t *errors;              // [1]
   int32_t P, T, S, V, player, tmn;
+  int32_t abort_on_error;       // 1: *errors != 0 (set by the checks launched
+                                // before) makes every env leave all state as is
 };
 
 // The move's four values and the range-check bits (high_low_trading.cc:264-271).
@@ -130,3 +132,6 @@ ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *p
 // astra_market_add_two_sided_quotes.
 int astra_game_move(astra_market *market, const GameMove &g, int32_t *const fill_fields[8],
                     int32_t *fill_rows, int32_t *fill_counts, hipStream_t stream);
+
+// The device the market lives on.
+int astra_game_device(const astra_market *market);

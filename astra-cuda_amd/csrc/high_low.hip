@@ -8,9 +8,9 @@
 // of the VecMarket matching kernel with the game's work fused around each
 // market's matching (game_move.h: checks, portfolio snapshot, BBO, last price,
 // telemetry, rewards). With check = 1 a small kernel checks the move's ranges
-// first and the host waits once and stops with an error, like the reference's
-// checks, before anything trades; with check = 0 nothing waits and the failed
-// checks stay in *errors.
+// first, the move kernel leaves every env untouched when any check failed, and
+// the host waits once, after the move, and returns the reference's error; with
+// check = 0 nothing waits and the failed checks stay in *errors.
 //
 // The kernel bodies are __host__ __device__ functions; the host-emulation build
 // (-DASTRA_HOST_EMULATION) runs them as loops over host memory.
@@ -185,15 +185,38 @@ int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *st
   g.player = t->player;
   g.tmn = t->trade_move_number;
   hipStream_t s = as_stream(stream);
-  if (t->check) {  // checks first, one wait, and stop like the reference (:264-271)
+  DeviceGuard dg(astra_game_device(market));
+  // With checks (the reference's behaviour, :264-271): a check launch, the error
+  // word to the host, then the move, which leaves every env as it is when any
+  // check failed. The host waits for the checks (with errors_host, only for
+  // them: the move runs meanwhile) and, on a failed check, restores the TID
+  // counter too, so the call has changed nothing when it returns the error.
+  g.abort_on_error = t->check ? 1 : 0;
+  int32_t tid_before = 0, bits = 0;
+  StreamMark checked;
+  if (t->check) {
     if ((rc = launch_check(g, M, s))) return rc;
-    int32_t bits = 0;
-    ASTRA_HIP_CHECK(rt_memcpy(&bits, t->errors, sizeof(bits), s), "error flags copy");
-    ASTRA_HIP_CHECK(rt_sync(s), "error flags wait");
-    if (bits) return fail(ASTRA_ERR_INVALID_ARGUMENT, std::string("high_low_trading.cc ") + check_text(bits));
+    if ((rc = astra_market_get_tid(market, &tid_before))) return rc;
+    if (t->errors_host) {
+      ASTRA_HIP_CHECK(rt_memcpy(t->errors_host, t->errors, sizeof(int32_t), s), "error flags copy");
+      ASTRA_HIP_CHECK(checked.record(s), "error flags event");
+    }
   }
   // the move itself: one launch of the matching kernel with the game's work fused
-  return astra_game_move(market, g, fields, t->fill_rows, t->fill_counts, s);
+  if ((rc = astra_game_move(market, g, fields, t->fill_rows, t->fill_counts, s))) return rc;
+  if (!t->check) return ASTRA_OK;
+  if (t->errors_host) {
+    ASTRA_HIP_CHECK(checked.wait(), "error flags wait");
+    bits = *t->errors_host;
+  } else {
+    ASTRA_HIP_CHECK(rt_memcpy(&bits, t->errors, sizeof(bits), s), "error flags copy");
+    ASTRA_HIP_CHECK(rt_sync(s), "error flags wait");
+  }
+  if (bits) {
+    astra_market_set_tid(market, tid_before);
+    return fail(ASTRA_ERR_INVALID_ARGUMENT, std::string("high_low_trading.cc ") + check_text(bits));
+  }
+  return ASTRA_OK;
 }
 
 int astra_high_low_observation(const astra_hl_observation *o, void *stream) {

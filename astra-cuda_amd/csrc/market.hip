@@ -461,6 +461,7 @@ struct MarketCtx {
   int32_t ns;             // ring position after the inserts
   bool bid_ok, ask_ok;
   GameQuote gq;           // the game's move (GAME only)
+  bool abort;             // GAME: a failed check stops the whole move
 };
 
 // The matching loop's state: everything a lane needs to resume the loop later.
@@ -477,6 +478,7 @@ struct LoopState {
   int32_t fc;                  // fills so far (-1 after an overflow)
   int32_t last_px;             // price of the last fill row written
   uint32_t emptied, forwarded; // diagnostic counts
+  uint32_t npass;
 };
 
 // The book as the loop sees it. GlobalBook: the market's arrays in global
@@ -551,7 +553,6 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
     ask_px = c.gq.ask_px;
     ask_sz = c.gq.ask_sz;
     cust = in.game.player;
-    game_before(in.game, c.pf, m, c.gq.bad);
   } else {
     bid_px = in.bid_px[m];
     bid_sz = in.bid_sz[m];
@@ -567,6 +568,9 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   int32_t ns = b.next_slot[m];
   const uint32_t tob = b.tob[m];
   const int32_t bsz0 = b.bbo[M + m], asz0 = b.bbo[3 * M + m];
+  c.abort = GAME && in.game.abort_on_error && *in.game.errors != 0;
+  if (GAME && c.abort) return;  // nothing written yet
+  if (GAME) game_before(in.game, c.pf, m, c.gq.bad);
 
   const bool bid_ok = bid_sz > 0 && (uint32_t)bid_px < (uint32_t)L;
   const bool ask_ok = ask_sz > 0 && (uint32_t)ask_px < (uint32_t)L;
@@ -685,7 +689,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   s.ahead = cross;
   s.fc = 0;
   s.last_px = 0;
-  s.emptied = s.forwarded = 0;
+  s.emptied = s.forwarded = s.npass = 0;
 }
 
 // The fill row of one pass (market.cu:172-218): the earlier TID rests (ties go
@@ -754,6 +758,7 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
   while (s.bb >= 0 && s.ba < L && s.bb >= s.ba) {
     if (s.bh >= (uint32_t)O || s.ah >= (uint32_t)O) break;  // NULL head (:155)
     if (passes++ >= budget || sink.full()) return false;
+    if (STATS) ++s.npass;
     // Records of heads that changed (the entry heads come from the prologue);
     // every size change is written through, so memory is current.
     if (!s.have_b) {
@@ -929,6 +934,9 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
     add_u64(b.stats + 2, (unsigned long long)s.emptied);
     add_u64(b.stats + 3, (unsigned long long)(s.fc < 0));
     add_u64(b.stats + 4, (unsigned long long)s.forwarded);
+    add_u64(b.stats + 5, (unsigned long long)s.npass);
+    add_u64(b.stats + 6, (unsigned long long)(BookMem::kStaged ? 1 : 0));
+    add_u64(b.stats + 7, (unsigned long long)(s.npass > 0 ? 1 : 0));
   }
 }
 
@@ -1065,8 +1073,8 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     MarketCtx c;
     LoopState<W> st;
     bool suspended = false;
-    if (m < b.M) {
-      quote_prologue<W, GAME>(b, ink, m, c, st);
+    if (m < b.M) quote_prologue<W, GAME>(b, ink, m, c, st);
+    if (m < b.M && !(GAME && c.abort)) {
       sink.base = m * (int64_t)b.F;
       const GlobalBook gb{c.lv, c.rec};
       if (match_loop<W, STATS>(st, c, gb, sink, out, bulk, budget)) {
@@ -1212,6 +1220,7 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
       MarketCtx c;
       LoopState<W> st;
       quote_prologue<W, GAME>(b, ink, m, c, st);
+      if (GAME && c.abort) continue;
       sink.base = m * (int64_t)b.F;
       const GlobalBook gb{c.lv, c.rec};
       const bool done = b.stats ? match_loop<W, true>(st, c, gb, sink, fo, bulk, budget)
@@ -1609,6 +1618,8 @@ int astra_market_add_two_sided_quotes_steps(
 }
 
 }  // extern "C"
+
+int astra_game_device(const astra_market *h) { return h ? h->device : 0; }
 
 int astra_game_move(astra_market *h, const GameMove &g, int32_t *const fill_fields[8],
                     int32_t *fill_rows, int32_t *fill_counts, hipStream_t stream) {

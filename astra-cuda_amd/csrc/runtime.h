@@ -41,6 +41,10 @@ struct DeviceGuard {
   explicit DeviceGuard(int) {}
 };
 inline void rt_device_sync(int) {}
+struct StreamMark {
+  hipError_t record(hipStream_t) { return hipSuccess; }
+  hipError_t wait() { return hipSuccess; }
+};
 #else
 inline hipError_t rt_device_count(int *n) { return hipGetDeviceCount(n); }
 inline hipError_t rt_memcpy(void *d, const void *s, size_t n, hipStream_t st) {
@@ -65,6 +69,23 @@ inline void rt_device_sync(int dev) {
   DeviceGuard g(dev);
   (void)hipDeviceSynchronize();
 }
+// A point in a stream the host can wait for while later work on the stream
+// runs (one cached event per host thread and device).
+struct StreamMark {
+  hipEvent_t ev = nullptr;
+  hipError_t record(hipStream_t st) {
+    static thread_local hipEvent_t cache[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!cache[dev] && (e = hipEventCreateWithFlags(&cache[dev], hipEventDisableTiming)) != hipSuccess)
+      return e;
+    ev = cache[dev];
+    return hipEventRecord(ev, st);
+  }
+  hipError_t wait() { return hipEventSynchronize(ev); }
+};
 #endif
 
 }  // namespace astra_rt

@@ -204,7 +204,7 @@ def main():
             snaps[2].add_two_sided_quotes(*rows[t], fills)
         torch.cuda.synchronize()
         snaps[2]._set_stats(None)
-    n_ins, n_fill, n_empty, n_ovf, n_ff = (int(x) for x in counters.cpu().tolist()[:5])
+    n_ins, n_fill, n_empty, n_ovf, n_ff, n_pass, n_staged, n_cross = (int(x) for x in counters.cpu().tolist())
 
     # ---- R: the same steps with the row layout of the FillBatch ----
     wall_rows = None
@@ -276,7 +276,8 @@ def main():
         "max_step_latency_ms": float(lat_ms.max()),
         "device_ms_per_step": {"quote_match": float(qm_ms.mean()), "get_bbos": float(bbo_ms.mean())},
         "work_per_step": {"inserts": n_ins / K, "fill_rows": n_fill / K, "levels_emptied": n_empty / K,
-                          "overflow_markets": n_ovf / K},
+                          "overflow_markets": n_ovf / K, "crossing_markets": n_cross / K,
+                          "loop_passes": n_pass / K, "staged_markets": n_staged / K},
         "roofline": {
             "kernel": "quote_match_kernel",
             "bound": "hbm",
@@ -408,7 +409,7 @@ def bench_game(args):
             "workload": f"config5_{cfg.name}", "envs": N, "players": P,
             "steps_per_player": cfg.steps_per_player, "max_contract_value": cfg.max_contract_value,
             "max_contracts_per_trade": cfg.max_contracts_per_trade,
-            "market_shape_LOFC": list(cfg.market_shape), "move_checks": "one sync per move",
+            "market_shape_LOFC": list(cfg.market_shape), "move_checks": "one host wait per move (for the checks)",
             "parallelism": "single GPU, one lane per env",
         },
         "market_steps_per_s": K / wall,

@@ -58,12 +58,17 @@ typedef struct astra_hl_trade {
                                      (astra_market_add_two_sided_quotes_rows) and the
                                      eight field pointers above are not used */
   int32_t *errors;                /* [1]: ASTRA_HL_ERR_* bits are OR-ed in; the caller zeroes it */
+  int32_t *errors_host;           /* NULL, or one int32 of pinned host memory: with check = 1
+                                     the error word is copied there right after the checks and
+                                     the host waits for that copy only, so the move kernel,
+                                     already queued, runs while the call returns */
   int32_t players, steps_per_player, max_contracts_per_trade, max_contract_value;
   int32_t player;                 /* the acting player (CurrentPlayer) */
   int32_t trade_move_number;      /* MoveNumber() - MaxChanceNodesInHistory() */
-  int32_t check;                  /* 1: sync once after the checks and return an error
-                                     without trading if any failed (the reference's
-                                     behaviour); 0: no sync, the errors stay in *errors */
+  int32_t check;                  /* 1: return the reference's error, with no state
+                                     changed, if any check failed (one host wait; the move
+                                     kernel then leaves every env as it is); 0: no wait,
+                                     the errors stay in *errors */
 } astra_hl_trade;
 
 /* HighLowTradingState::ApplyPlayerTrading (high_low_trading.cc:247-329) for all N

@@ -182,9 +182,11 @@ int astra_market_to_string(const astra_market *market, int32_t market_id, char *
 
 /* Diagnostic, no counterpart in the reference: while `counters` (int64 [8],
  * device memory, caller-zeroed) is set, astra_market_add_two_sided_quotes also
- * adds to [0..4] the accepted order inserts, fill rows written (F for a market
- * that overflowed), price levels emptied, markets that overflowed, and
- * overflows reached by fast-forwarding a repeating loop state ([5..7] unused).
+ * adds to [0..7] the accepted order inserts, fill rows written (F for a market
+ * that overflowed), price levels emptied, markets that overflowed, overflows
+ * reached by fast-forwarding a repeating loop state, matching-loop passes,
+ * markets finished from a staged (LDS) copy of their book, and markets whose
+ * book crossed (that entered the matching loop).
  * These are the work counts of the algorithmic-byte roofline. NULL switches it
  * off (the default); the timed path never has it on. */
 int astra_market_set_stats(astra_market *market, int64_t *counters);

@@ -272,6 +272,7 @@ class EmuHighLow:
         self.immediate_rewards = z(N, P)
         self.rewards_since_last_action = z(N, P)
         self.errors = z(1)
+        self.errors_host = z(1)
         self._HLTrade, self._HLObservation = HLTrade, HLObservation
 
     def trade(self, move, player, tmn, check=1):
@@ -280,8 +281,9 @@ class EmuHighLow:
         ptr = lambda a: a.ctypes.data  # noqa: E731
         for name in ("player_last_positions", "target_positions", "contract_values",
                      "player_contract_over_time", "market_contract_over_time", "immediate_rewards",
-                     "rewards_since_last_action", "errors"):
-            setattr(t, name, ptr(getattr(self, name)))
+                     "rewards_since_last_action", "errors", "errors_host"):
+            a = getattr(self, name)
+            setattr(t, name, None if a is None else ptr(a))
         t.move = ptr(self.move)
         if isinstance(self.fills, EmuRowFills):
             t.fill_rows, t.fill_counts = ptr(self.fills.rows), ptr(self.fills.fill_counts)

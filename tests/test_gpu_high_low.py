@@ -118,9 +118,16 @@ def test_gpu_move_checks():
         s.apply_action(_t(np.repeat(c, 5, axis=0)))
     bad = np.tile(np.array([[12, 18, 2, 1]], np.int32), (5, 1))
     bad[3, 3] = 6  # ask size above max_contracts_per_trade
+    names = ("player_last_positions", "player_contract_over_time", "market_contract_over_time",
+             "immediate_rewards", "rewards_since_last_action")
+    before = {n: getattr(s, n).clone() for n in names}
+    ws = s.market._ws.clone()
     with pytest.raises(RuntimeError, match="Astra Fatal Error.*ask_sizes"):
         s.apply_action(_t(bad))
     assert s.move_number() == MAX_CHANCE_NODES and s.market.global_tid == 0
+    assert torch.equal(s.market._ws, ws)  # the move kernel ran and left every env as it was
+    for n, v in before.items():
+        assert torch.equal(getattr(s, n), v), n
     s.apply_action(_t(np.tile(np.array([[12, 18, 2, 1]], np.int32), (5, 1))))  # good move goes through
     assert s.move_number() == MAX_CHANCE_NODES + 1
     # unchecked: no sync per move; check_errors reports afterwards

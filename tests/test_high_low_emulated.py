@@ -78,17 +78,35 @@ def test_emulated_hand_game():
             assert e.observation(HAND_GAME["obs_player"], 1)[0].tolist() == HAND_GAME["obs"]
 
 
-def test_emulated_checks_flag_and_stop():
+@pytest.mark.parametrize("host_word", [True, False], ids=["errors_host", "no_errors_host"])
+def test_emulated_checks_flag_and_stop(host_word):
     N, P, T, S, cM, V = 6, 4, 2, 5, 5, 30
     o = OracleHighLow(N, P, T, S, cM, V)
     e = EmuHighLow(N, P, T, S, cM, V, (o.L, o.O, o.F, o.C))
+    if not host_word:
+        e.errors_host = None
     mv = np.tile(np.array([[12, 18, 2, 1]], np.int32), (N, 1))
     mv[2, 2] = S + 1     # bid size above max_contracts_per_trade
     mv[4, 0] = 0         # bid price not > 0
-    rc = e.trade(mv, 0, 0, check=1)
+    e.trade(np.tile(np.array([[12, 18, 2, 1]], np.int32), (N, 1)), 0, 0, check=1)  # a good move first
+    e.errors[0] = 0
+    names = ("player_last_positions", "player_contract_over_time", "market_contract_over_time",
+             "immediate_rewards", "rewards_since_last_action")
+    before = {n: getattr(e, n).copy() for n in names}
+    ws, tid = e.market.ws.copy(), e.market.global_tid
+    fills = {f: np.array(getattr(e.fills, f)).copy() for f in e.fills.FIELDS}
+    bbo = {f: getattr(e.bbo, f).copy() for f in e.bbo.FIELDS}
+    rc = e.trade(mv, 1, 1, check=1)
     assert rc != 0
     assert e.errors[0] == (1 << 0) | (1 << 6)
-    assert e.market.global_tid == 0 and not e.fills.fill_counts.any()  # nothing traded
+    # nothing changed: the book, the TID counter, fills, BBOs and every state array
+    assert np.array_equal(e.market.ws, ws) and e.market.global_tid == tid
+    for f, v in fills.items():
+        assert np.array_equal(np.array(getattr(e.fills, f)), v), f
+    for f, v in bbo.items():
+        assert np.array_equal(getattr(e.bbo, f), v), f
+    for n, v in before.items():
+        assert np.array_equal(getattr(e, n), v), n
     e.errors[0] = 0
-    assert e.trade(mv, 0, 0, check=0) == 0  # no check: trades, flag kept for the caller
-    assert e.errors[0] == (1 << 0) | (1 << 6) and e.market.global_tid == 2
+    assert e.trade(mv, 1, 1, check=0) == 0  # no check: trades, flag kept for the caller
+    assert e.errors[0] == (1 << 0) | (1 << 6) and e.market.global_tid == tid + 2
