@@ -264,6 +264,11 @@ ASTRA_HD uint32_t level_word(const uint16_t *lv, int32_t price, int side) {
   return *reinterpret_cast<const uint32_t *>(lv + (size_t)price * 4 + 2 * side);
 }
 
+// The head slot of level `price` on `side` (the low half of its word).
+ASTRA_HD uint32_t level_head(const uint16_t *lv, int32_t price, int side) {
+  return lv[(size_t)price * 4 + 2 * side];
+}
+
 ASTRA_HD void store_level_word(uint16_t *lv, int32_t price, int side, uint32_t w) {
   *reinterpret_cast<uint32_t *>(lv + (size_t)price * 4 + 2 * side) = w;
 }
@@ -473,7 +478,7 @@ struct LoopState {
   uint4 brec, arec;            // records of bh / ah when have_b / have_a
   bool have_b, have_a;
   int pb, pa;                  // next levels whose words were read ahead
-  uint32_t pbw, paw;
+  uint32_t pbh, pah;           // their head slots
   bool ahead;                  // read-ahead issued for the current levels
   int32_t fc;                  // fills so far (-1 after an overflow)
   int32_t last_px;             // price of the last fill row written
@@ -492,6 +497,7 @@ struct GlobalBook {
   ASTRA_HD uint4 record(uint32_t s) const { return rec[s]; }
   ASTRA_HD int32_t size(uint32_t s) const { return reinterpret_cast<const int32_t *>(rec + s)[0]; }
   ASTRA_HD uint32_t word(int32_t p, int side) const { return level_word(lv, p, side); }
+  ASTRA_HD uint32_t head(int32_t p, int side) const { return level_head(lv, p, side); }
   ASTRA_HD void set_size(uint32_t s, int32_t v) const {
     reinterpret_cast<int32_t *>(rec + s)[0] = v;
   }
@@ -506,6 +512,7 @@ struct StagedBook {
   ASTRA_HD uint4 record(uint32_t s) const { return srec[s]; }
   ASTRA_HD int32_t size(uint32_t s) const { return reinterpret_cast<const int32_t *>(srec + s)[0]; }
   ASTRA_HD uint32_t word(int32_t p, int side) const { return level_word(slv, p, side); }
+  ASTRA_HD uint32_t head(int32_t p, int side) const { return level_head(slv, p, side); }
   ASTRA_HD void set_size(uint32_t s, int32_t v) const {
     reinterpret_cast<int32_t *>(srec + s)[0] = v;
   }
@@ -592,7 +599,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   if (cross && !bid_top && hb0 < (uint32_t)O) hrb = rec[hb0];
   if (cross && !ask_top && ha0 < (uint32_t)O) hra = rec[ha0];
   int pb = -1, pa = L;
-  uint32_t pbw = 0xFFFFFFFFu, paw = 0xFFFFFFFFu;
+  uint32_t pbh = kNull16, pah = kNull16;
   if (cross) {
     uint64_t t[W];
 #pragma unroll
@@ -600,13 +607,13 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
     if (bid_ok) mask_set<W>(t, bid_px);
     mask_clear<W>(t, bb);
     pb = mask_highest<W>(t);
-    if (pb >= 0) pbw = level_word(lv, pb, 0);
+    if (pb >= 0) pbh = level_head(lv, pb, 0);
 #pragma unroll
     for (int i = 0; i < W; ++i) t[i] = s.am[i];
     if (ask_ok) mask_set<W>(t, ask_px);
     mask_clear<W>(t, ba);
     pa = mask_lowest<W>(t, L);
-    if (pa < L) paw = level_word(lv, pa, 1);
+    if (pa < L) pah = level_head(lv, pa, 1);
   }
 
   // ---- add: bid first, then ask (market.cu:44-70, 73-99) ----
@@ -680,12 +687,12 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   }
   s.have_b = s.have_a = true;
   // the next levels read ahead, as the inserts left their heads
-  if (bid_ok && pb == bid_px && (bword >> 16) == kNull16) pbw = bslot | (bslot << 16);
-  if (ask_ok && pa == ask_px && (aword >> 16) == kNull16) paw = aslot | (aslot << 16);
+  if (bid_ok && pb == bid_px && (bword >> 16) == kNull16) pbh = bslot;
+  if (ask_ok && pa == ask_px && (aword >> 16) == kNull16) pah = aslot;
   s.pb = pb;
   s.pa = pa;
-  s.pbw = pbw;
-  s.paw = paw;
+  s.pbh = pbh;
+  s.pah = pah;
   s.ahead = cross;
   s.fc = 0;
   s.last_px = 0;
@@ -775,12 +782,14 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
       for (int i = 0; i < W; ++i) t[i] = s.bm[i];
       mask_clear<W>(t, s.bb);
       s.pb = mask_highest<W>(t);
-      if (s.pb >= 0) s.pbw = bk.word(s.pb, 0);
 #pragma unroll
       for (int i = 0; i < W; ++i) t[i] = s.am[i];
       mask_clear<W>(t, s.ba);
       s.pa = mask_lowest<W>(t, L);
-      if (s.pa < L) s.paw = bk.word(s.pa, 1);
+      // both heads in one round trip: unconditional loads (level 0 stands in
+      // for a side with no next level), nothing waits on them in this block
+      s.pbh = bk.head(s.pb >= 0 ? s.pb : 0, 0);
+      s.pah = bk.head(s.pa < L ? s.pa : 0, 1);
       s.ahead = true;
     }
     // On the staged book a pass costs instructions, not memory round trips,
@@ -842,7 +851,7 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
         mask_clear<W>(s.bm, s.bb);
         if (STATS) ++s.emptied;
         s.bb = mask_highest<W>(s.bm);  // the level read ahead
-        s.bh = s.bb >= 0 ? ((s.bb == s.pb ? s.pbw : bk.word(s.bb, 0)) & kNull16) : kNull16;
+        s.bh = s.bb >= 0 ? ((s.bb == s.pb ? s.pbh : bk.word(s.bb, 0)) & kNull16) : kNull16;
         s.have_b = false;
         s.ahead = false;
       } else if (nh != s.bh) {
@@ -858,7 +867,7 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
         mask_clear<W>(s.am, s.ba);
         if (STATS) ++s.emptied;
         s.ba = mask_lowest<W>(s.am, L);
-        s.ah = s.ba < L ? ((s.ba == s.pa ? s.paw : bk.word(s.ba, 1)) & kNull16) : kNull16;
+        s.ah = s.ba < L ? ((s.ba == s.pa ? s.pah : bk.word(s.ba, 1)) & kNull16) : kNull16;
         s.have_a = false;
         s.ahead = false;
       } else if (nh != s.ah) {

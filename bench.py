@@ -392,6 +392,10 @@ def bench_game(args):
     game_bytes = N * ((16 + 4 + 4 + 16 * P) + (16 + 4 + 28 + 24 * P))
     step_bytes = (24.0 * N * K + 32.0 * n_ins + 109.0 * n_fill + 8.0 * n_empty) / K + game_bytes
     achieved = step_bytes / (step_ms * 1e-3) / 1e9
+    traffic, traffic_src = (None, None)
+    if N == cfg.envs:
+        traffic, traffic_src = profile_traffic(f"game_move_config5_{cfg.name}_kernel_trace.md",
+                                               "quote_match_kernel<2, false, true, false>")
     result = {
         "metric": "quote-matches/sec and market-steps/sec at 100k markets; p50 step latency",
         "value": N * K / wall,
@@ -422,7 +426,7 @@ def bench_game(args):
         "roofline": {
             "kernel": "quote_match_kernel with the game move fused (one launch per move)", "bound": "hbm",
             "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None, "algorithmic_bytes_per_launch": step_bytes,
+            "traffic": traffic, "traffic_source": traffic_src, "algorithmic_bytes_per_launch": step_bytes,
         },
     }
     if not args.no_cpu_baseline:
@@ -459,16 +463,11 @@ def game_cpu_baseline(args, cfg, chance, host_moves, N, W, K):
             "host_cpu": model, "host_cpus_available": avail}
 
 
-def measured_traffic(cfg, M, bbo):
-    """HBM bytes per matching-kernel launch for this workload, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None."""
-    if M != cfg.M or bbo != cfg.bbo_every_step:
-        return None, None
-    words = 1
-    while words * 64 < cfg.L:
-        words *= 2
-    key = f"traffic_bytes_per_launch[void quote_match_kernel<{words}, false>]:"
-    path = os.path.join(ROOT, "profiles", f"quote_match_config{cfg.index}_{cfg.name}_hbm_traffic.md")
+def profile_traffic(profile: str, kernel: str):
+    """HBM bytes per launch of `kernel` from a committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary under profiles/ (copy-calibrated), or (None, None)."""
+    key = f"traffic_bytes_per_launch[void {kernel}]:"
+    path = os.path.join(ROOT, "profiles", profile)
     try:
         with open(path) as f:
             for line in f:
@@ -477,6 +476,17 @@ def measured_traffic(cfg, M, bbo):
     except OSError:
         pass
     return None, None
+
+
+def measured_traffic(cfg, M, bbo):
+    """HBM bytes per matching-kernel launch for this workload (see profile_traffic)."""
+    if M != cfg.M or bbo != cfg.bbo_every_step:
+        return None, None
+    words = 1
+    while words * 64 < cfg.L:
+        words *= 2
+    return profile_traffic(f"quote_match_config{cfg.index}_{cfg.name}_hbm_traffic.md",
+                           f"quote_match_kernel<{words}, false, false, false>")
 
 
 def cpu_baseline(args, cfg, host, M, W, K, bbo):
