@@ -116,6 +116,26 @@ def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, lay
         assert r["overflows"] > 0
 
 
+@pytest.mark.parametrize("per_wave,stage_budget", [(1, 1), (7, None), (32, 1), (33, None)])
+def test_gpu_markets_per_wavefront(per_wave, stage_budget):
+    """Fewer markets per wavefront than 64 (ASTRA_MARKET_PER_WAVE, read at creation):
+    the same results, with staging (its cooperative copies use all 64 lanes)."""
+    M, L, O, F, C, steps = 300, 16, 3, 4, 4, 150
+    _log(f"per_wave {per_wave} stage budget {stage_budget}")
+    rng = np.random.default_rng(per_wave)
+
+    def gen(t):
+        base = rng.integers(0, L - 12, 1)[0]
+        bid = (base + rng.integers(-1, 13, M)).astype(np.int32)
+        ask = (base + rng.integers(-1, 13, M)).astype(np.int32)
+        return (bid, rng.integers(0, 8, M).astype(np.int32), ask, rng.integers(0, 8, M).astype(np.int32),
+                rng.integers(0, C, M).astype(np.int32))
+
+    r = run_parity(M, L, O, F, C, steps, gen, full_every=50, label=f"per_wave {per_wave}",
+                   stage_budget=stage_budget, per_wave=per_wave)
+    assert r["fill_rows"] > 0
+
+
 def test_gpu_reset_clear_clone_and_to_string():
     """Reset / ClearQuotes / copy constructor / ToString interleaved with trading."""
     from astra_cuda import order_matching as aom
