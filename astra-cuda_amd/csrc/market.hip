@@ -487,6 +487,36 @@ struct LoopState {
   uint32_t npass;
 };
 
+// What one step of a multi-step launch hands its market's next step, in
+// registers: the market's coalesced words as the step's epilogue left them
+// (masks, ring position, best-level heads and sizes), so the next prologue
+// skips its first round trip, and the next step's quotes, loaded ahead.
+// (The masks are carried for up to 256 levels; wider ones would spill
+// registers, so those markets reload their coalesced words every step.)
+template <int W>
+struct Carry {
+  static constexpr bool kState = W <= 4;
+  uint64_t bm[W], am[W];
+  int32_t ns, bsz, asz;
+  uint32_t tob;
+  int32_t q[5];
+  bool state, quotes;
+};
+
+// Step k's quotes of market m into the carry (nothing past the last step).
+template <int W>
+ASTRA_HD void load_next_quotes(const QuoteIn &in, int64_t M, int32_t k, int32_t steps, int64_t m,
+                               Carry<W> &cy) {
+  cy.quotes = k < steps;
+  if (!cy.quotes) return;
+  const int64_t o = (int64_t)k * M + m;
+  cy.q[0] = in.bid_px[o];
+  cy.q[1] = in.bid_sz[o];
+  cy.q[2] = in.ask_px[o];
+  cy.q[3] = in.ask_sz[o];
+  cy.q[4] = in.cust[o];
+}
+
 // The book as the loop sees it. GlobalBook: the market's arrays in global
 // memory. StagedBook: a copy of the market's records and level words (in LDS
 // on the GPU) that the loop reads and writes; it is copied back to global
@@ -536,9 +566,9 @@ struct StagedBook {
 // all at once, before the inserts write anything; the values are then patched
 // for what the inserts wrote (a slot the ring reuses, a tail link), so the
 // first loop pass starts with everything in registers.
-template <int W, bool GAME>
+template <int W, bool GAME, bool CARRY = false>
 ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, MarketCtx &c,
-                             LoopState<W> &s) {
+                             LoopState<W> &s, const Carry<W> *cy = nullptr) {
   const int64_t M = b.M;
   const int32_t L = b.L, O = b.O;
   c.m = m;
@@ -554,7 +584,13 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
 
   // ---- round trip 1 ----
   int32_t bid_px, bid_sz, ask_px, ask_sz, cust;
-  if (GAME) {
+  if (CARRY && cy->quotes) {
+    bid_px = cy->q[0];
+    bid_sz = cy->q[1];
+    ask_px = cy->q[2];
+    ask_sz = cy->q[3];
+    cust = cy->q[4];
+  } else if (GAME) {
     c.gq = game_quote(in.game, m);
     bid_px = c.gq.bid_px;
     bid_sz = c.gq.bid_sz;
@@ -568,14 +604,29 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
     ask_sz = in.ask_sz[m];
     cust = in.cust[m];
   }
+  int32_t ns, bsz0, asz0;
+  uint32_t tob;
+  if (CARRY && Carry<W>::kState && cy->state) {
 #pragma unroll
-  for (int i = 0; i < W; ++i) {
-    s.bm[i] = b.masks[(int64_t)i * M + m];
-    s.am[i] = b.masks[(int64_t)(W + i) * M + m];
+    for (int i = 0; i < W; ++i) {
+      s.bm[i] = cy->bm[i];
+      s.am[i] = cy->am[i];
+    }
+    ns = cy->ns;
+    tob = cy->tob;
+    bsz0 = cy->bsz;
+    asz0 = cy->asz;
+  } else {
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      s.bm[i] = b.masks[(int64_t)i * M + m];
+      s.am[i] = b.masks[(int64_t)(W + i) * M + m];
+    }
+    ns = b.next_slot[m];
+    tob = b.tob[m];
+    bsz0 = b.bbo[M + m];
+    asz0 = b.bbo[3 * M + m];
   }
-  int32_t ns = b.next_slot[m];
-  const uint32_t tob = b.tob[m];
-  const int32_t bsz0 = b.bbo[M + m], asz0 = b.bbo[3 * M + m];
   c.abort = GAME && in.game.abort_on_error && *in.game.errors != 0;
   if (GAME && c.abort) return;  // nothing written yet
   if (GAME) game_before(in.game, c.pf, m, c.gq.bad);
@@ -900,7 +951,8 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
 template <int W, bool STATS, bool GAME, bool MULTI, class BookMem>
 ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx &c,
                              const LoopState<W> &s, FillSink &sink, const BookMem &bk,
-                             const GameMove &game, const StepOut &so) {
+                             const GameMove &game, const StepOut &so,
+                             Carry<W> *cy = nullptr, bool last = true) {
   const int64_t M = b.M, m = c.m;
   const int32_t L = c.L, O = c.O;
   // Loads first, then plain stores and the fill rows with their portfolio
@@ -910,20 +962,40 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
   if (s.bb >= 0 && s.bh < (uint32_t)O) obs = s.have_b ? (int32_t)s.brec.x : bk.size(s.bh);
   if (s.ba < L && s.ah < (uint32_t)O) oas = s.have_a ? (int32_t)s.arec.x : bk.size(s.ah);
   out.counts[m] = s.fc;
+  // (a multi-step launch keeps these in registers and stores them after its
+  // last step only)
+  const bool store = !MULTI || last || !Carry<W>::kState;
+  if (store) {
 #pragma unroll
-  for (int i = 0; i < W; ++i) {
-    b.masks[(int64_t)i * M + m] = s.bm[i];
-    b.masks[(int64_t)(W + i) * M + m] = s.am[i];
+    for (int i = 0; i < W; ++i) {
+      b.masks[(int64_t)i * M + m] = s.bm[i];
+      b.masks[(int64_t)(W + i) * M + m] = s.am[i];
+    }
+    b.next_slot[m] = c.ns;
   }
-  b.next_slot[m] = c.ns;
   sink.flush(out, c.pf, c.C);  // overlaps the loads above
   const int32_t obp = (s.bb >= 0 && s.bh < (uint32_t)O) ? s.bb : ASTRA_NULL_INDEX;
   const int32_t oap = (s.ba < L && s.ah < (uint32_t)O) ? s.ba : ASTRA_NULL_INDEX;
-  b.bbo[m] = obp;
-  b.bbo[M + m] = obs;
-  b.bbo[2 * M + m] = oap;
-  b.bbo[3 * M + m] = oas;
-  b.tob[m] = ((s.bb >= 0 ? s.bh : kNull16) & kNull16) | ((s.ba < L ? s.ah : kNull16) << 16);
+  const uint32_t tob = ((s.bb >= 0 ? s.bh : kNull16) & kNull16) | ((s.ba < L ? s.ah : kNull16) << 16);
+  if (store) {
+    b.bbo[m] = obp;
+    b.bbo[M + m] = obs;
+    b.bbo[2 * M + m] = oap;
+    b.bbo[3 * M + m] = oas;
+    b.tob[m] = tob;
+  }
+  if (MULTI && Carry<W>::kState && cy) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      cy->bm[i] = s.bm[i];
+      cy->am[i] = s.am[i];
+    }
+    cy->ns = c.ns;
+    cy->tob = tob;
+    cy->bsz = obs;
+    cy->asz = oas;
+    cy->state = true;
+  }
   if (GAME) {
     const int32_t bbo[4] = {obp, obs, oap, oas};
     game_after(game, c.gq, c.pf, m, bbo, s.fc, s.last_px);
@@ -1078,21 +1150,25 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
   sink.lds = wave_lds;
   sink.lane = lane;
 #endif
+  Carry<W> cy;
+  cy.state = cy.quotes = false;
   for (int32_t k = 0; k < (MULTI ? steps : 1); ++k) {
     QuoteIn ink = in;
     StepOut sok = so;
     if (MULTI) step_views(in, so, b.M, steps, k, ink, sok);
+    const bool last = k + 1 == (MULTI ? steps : 1);
     Bulk bulk;
     bulk.count = 0;
     MarketCtx c;
     LoopState<W> st;
     bool suspended = false;
-    if (m < b.M) quote_prologue<W, GAME>(b, ink, m, c, st);
+    if (m < b.M) quote_prologue<W, GAME, MULTI>(b, ink, m, c, st, &cy);
+    if (MULTI && m < b.M) load_next_quotes(in, b.M, k + 1, steps, m, cy);
     if (m < b.M && !(GAME && c.abort)) {
       sink.base = m * (int64_t)b.F;
       const GlobalBook gb{c.lv, c.rec};
       if (match_loop<W, STATS>(st, c, gb, sink, out, bulk, budget)) {
-        quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, gb, ink.game, sok);
+        quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, gb, ink.game, sok, &cy, last);
       } else {
         sink.flush(out, c.pf, c.C);  // frees the LDS for staging
         suspended = true;
@@ -1158,7 +1234,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
       for (int32_t j = lane; j < b.L; j += 64) glv[j] = slv[j];
       if (lane == src) {
         sink.base = rb.base;
-        quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, sb, ink.game, sok);
+        quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, sb, ink.game, sok, &cy, last);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -1232,25 +1308,32 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   std::vector<uint4> srec(staged ? (size_t)h->O : 0);
   std::vector<uint16_t> slv(staged ? (size_t)h->L * 4 : 0);
   std::vector<int32_t> rows((size_t)kStageRows * 8);
+  std::vector<Carry<W>> carry(MULTI ? (size_t)b.M : 0);
+  for (auto &cy : carry) cy.state = cy.quotes = false;
   for (int32_t k = 0; k < (MULTI ? steps : 1); ++k) {
     QuoteIn ink = in;
     StepOut sok = so;
     if (MULTI) step_views(in, so, b.M, steps, k, ink, sok);
+    const bool last = k + 1 == (MULTI ? steps : 1);
     for (int64_t m = 0; m < b.M; ++m) {
       Bulk bulk;
       bulk.count = 0;
       FillSink sink;
       MarketCtx c;
       LoopState<W> st;
-      quote_prologue<W, GAME>(b, ink, m, c, st);
+      Carry<W> *cy = MULTI ? &carry[(size_t)m] : nullptr;
+      quote_prologue<W, GAME, MULTI>(b, ink, m, c, st, cy);
+      if (MULTI) load_next_quotes(in, b.M, k + 1, steps, m, *cy);
       if (GAME && c.abort) continue;
       sink.base = m * (int64_t)b.F;
       const GlobalBook gb{c.lv, c.rec};
       const bool done = b.stats ? match_loop<W, true>(st, c, gb, sink, fo, bulk, budget)
                                 : match_loop<W, false>(st, c, gb, sink, fo, bulk, budget);
       if (done) {
-        if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok);
-        else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok);
+        if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok, cy,
+                                                           last);
+        else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok, cy,
+                                                         last);
       } else {  // the second pass, as on the GPU
         sink.flush(fo, c.pf, c.C);
         std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
@@ -1268,8 +1351,10 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
         std::memcpy(c.rec, srec.data(), (size_t)h->O * 16);
         std::memcpy(c.lv, slv.data(), (size_t)h->L * 8);
         sink.base = rb.base;
-        if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok);
-        else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok);
+        if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok, cy,
+                                                           last);
+        else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok, cy,
+                                                         last);
       }
       if (bulk.count > 0) write_bulk_host(fo, bulk);
     }
