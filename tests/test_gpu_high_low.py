@@ -140,6 +140,30 @@ def test_gpu_move_checks():
     s2.check_errors()  # cleared
 
 
+def test_gpu_move_checks_many_blocks():
+    """The check kernel over 300,000 envs (1024 blocks, several envs per thread): the
+    last block publishes the OR of every block's bits; a failed check anywhere stops
+    the move, the message names the first failed check in the reference's order, and
+    the calls after it (the block counter reset) behave."""
+    N = 300_000
+    prm = dict(HAND_GAME["params"], num_markets=N)
+    s = _game(prm).new_initial_state()
+    for c in HAND_GAME["chance"]:
+        s.apply_action(_t(np.repeat(c, N, axis=0)))
+    good = np.tile(np.array([[12, 18, 2, 1]], np.int32), (N, 1))
+    s.apply_action(_t(good))
+    bad = good.copy()
+    bad[N - 1, 3] = 6  # ask size above max in the last env
+    with pytest.raises(RuntimeError, match="max\\(ask_sizes\\)"):
+        s.apply_action(_t(bad))
+    bad[0, 1] = 0      # ask price not > 0 in the first env: earlier in the reference's order
+    with pytest.raises(RuntimeError, match="min\\(ask_prices\\)"):
+        s.apply_action(_t(bad))
+    assert s.move_number() == MAX_CHANCE_NODES + 1 and s.market.global_tid == 2
+    s.apply_action(_t(good))
+    assert s.move_number() == MAX_CHANCE_NODES + 2 and s.market.global_tid == 4
+
+
 def test_gpu_text_renderings():
     """to_string / observation_string / information_state_string: the hand-derived
     text, and the oracle's on a random game (every few moves, several envs)."""
