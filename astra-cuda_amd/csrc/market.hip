@@ -1286,12 +1286,15 @@ __global__ __launch_bounds__(kFillThreads) void fill_u32_kernel(uint32_t *dst, i
 inline unsigned grid_for(int64_t n, int block) { return (unsigned)((n + block - 1) / block); }
 
 // Markets per wavefront of the matching kernel: the handle's setting
-// (ASTRA_MARKET_PER_WAVE at creation, 1-64) if any, else 64, or 32 for the game
-// move: at 10,000 envs its 157 full wavefronts leave most SIMDs idle, and
-// half-full ones end sooner (each waits for the slowest of fewer markets), 6%
-// faster per move on MI355X; a full grid (config 3) is 6% slower at 32.
+// (ASTRA_MARKET_PER_WAVE at creation, 1-64) if any, else 64, or 32 for a game
+// move over at most 65,536 envs (2,048 half-full wavefronts, what 256 CUs hold
+// at 8 each): at 10,000 envs the 157 full wavefronts leave most SIMDs idle,
+// and half-full ones end sooner (each waits for the slowest of fewer markets),
+// 6% faster per move on MI355X; a grid that fills the GPU (config 3) is 6%
+// slower at 32.
 int32_t markets_per_wave(const astra_market *h, bool game) {
-  return h->per_wave ? h->per_wave : (game ? 32 : 64);
+  if (h->per_wave) return h->per_wave;
+  return (game && h->M <= 32 * 2048) ? 32 : 64;
 }
 
 template <int W, bool GAME, bool MULTI>

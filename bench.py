@@ -55,7 +55,10 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=900, help="timed steps K")
     ap.add_argument("--warmup", type=int, default=100, help="untimed warm-up steps W")
     ap.add_argument("--config", type=int, default=3,
-                    help="BASELINE.json config index (2, 3 or 4; 5 = the high-low game step)")
+                    help="BASELINE.json config index (2, 3 or 4; 5 = the high-low game step; "
+                         "6 = the reference's own game benchmark workload, "
+                         "src/tests/benchmarks/high_low_benchmark.py)")
+    ap.add_argument("--episodes", type=int, default=30, help="config 6: episodes timed")
     ap.add_argument("--markets", type=int, default=0, help="override the config's market count")
     ap.add_argument("--no-bbo", action="store_true", help="do not call get_bbos every step")
     ap.add_argument("--latency-steps", type=int, default=300)
@@ -110,6 +113,8 @@ def main():
 
     if args.config == 5:
         return bench_game(args)
+    if args.config == 6:
+        return bench_game_reference(args)
 
     import numpy as np
     import torch
@@ -431,6 +436,104 @@ def bench_game(args):
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = game_cpu_baseline(args, cfg, chance, host_moves, N, W, K)
+    print(json.dumps(result), flush=True)
+
+
+# src/tests/README.md:142,144-145: the reference's best game figure, RTX 5090
+REF_GAME_FPS_RTX5090 = 164_402_193
+REF_GAME_ENVS = 262_144
+
+
+def bench_game_reference(args):
+    """The reference's own game benchmark (src/tests/benchmarks/high_low_benchmark.py:
+    run_benchmark, :169-246, with its parameters, :305-314) on this engine: per
+    episode reset, the four fixed chance moves and 40 trading steps of
+    fill_observation_tensor + apply_action (input checks on) + fill_rewards +
+    fill_rewards_since_last_action, then fill_returns; random trading actions
+    (prices 1-10, sizes 0-1) pre-generated on the device. FPS = trading steps x
+    envs / total wall time, as there (:233). One warm-up episode is not timed."""
+    import numpy as np
+    import torch
+    import astra_cuda as astra
+
+    N = args.markets or REF_GAME_ENVS
+    P, T, V = 5, 8, 10
+    params = {"steps_per_player": T, "max_contracts_per_trade": 1, "customer_max_size": 2,
+              "max_contract_value": V, "players": P, "num_markets": N, "threads_per_block": 256,
+              "device_id": 0}
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    astra.register_games()
+    game = astra.load_game("high_low_trading", params)
+    state = game.new_initial_state()
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    steps = T * P
+    actions = torch.zeros((steps, N, 4), dtype=torch.int32, device=dev)
+    actions[:, :, 0:2] = torch.randint(1, V + 1, (steps, N, 2), dtype=torch.int32, device=dev, generator=g)
+    actions[:, :, 2:4] = torch.randint(0, 2, (steps, N, 2), dtype=torch.int32, device=dev, generator=g)
+    cand = torch.zeros((N, 2), dtype=torch.int32, device=dev)
+    cand[:, 0], cand[:, 1] = 3, 8
+    settle = torch.arange(N, dtype=torch.int32, device=dev) % 2
+    perm = torch.arange(P, dtype=torch.int32, device=dev).unsqueeze(0).repeat(N, 1)
+    cust = torch.zeros((N, P - 3), dtype=torch.int32, device=dev)
+    cust[:, 0] = -2
+    cust[:, 1] = 2
+    obs = torch.zeros(game.observation_tensor_shape(), dtype=torch.float32, device=dev)
+    imm = torch.zeros((N, P), dtype=torch.float32, device=dev)
+    mine = torch.zeros((N,), dtype=torch.float32, device=dev)
+    ret = torch.zeros((N, P), dtype=torch.float32, device=dev)
+
+    def episode(step_ms):
+        state.reset()
+        for a in (cand, settle, perm, cust):
+            state.apply_action(a)
+        k = 0
+        while not state.is_terminal():
+            player = state.current_player()
+            h0 = time.perf_counter()
+            state.fill_observation_tensor(obs)
+            state.apply_action(actions[k])
+            state.fill_rewards(imm)
+            state.fill_rewards_since_last_action(mine, player)
+            step_ms.append((time.perf_counter() - h0) * 1e3)
+            k += 1
+        state.fill_returns(ret)
+        return k
+
+    episode([])
+    torch.cuda.synchronize()
+    log(f"config 6: {N} envs, warm-up episode done; timing {args.episodes} episodes")
+    step_ms = []
+    t0 = time.perf_counter()
+    total = sum(episode(step_ms) for _ in range(args.episodes))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    fps = total * N / wall
+    result = {
+        "metric": "game env-steps/sec (the reference's high_low_benchmark.py workload)",
+        "value": fps,
+        "unit": "env-steps/s",
+        "n_gpus": 1,
+        "steps": total,
+        "warmup": steps,
+        "ms_per_step": wall / total * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": "synthetic",
+        "config": {"workload": "config6_reference_game_benchmark", "envs": N, "players": P,
+                   "steps_per_player": T, "max_contract_value": V, "max_contracts_per_trade": 1,
+                   "customer_max_size": 2, "episodes": args.episodes,
+                   "parallelism": "single GPU, one lane per env"},
+        "avg_step_ms": float(np.mean(step_ms)),
+        "max_step_ms": float(np.max(step_ms)),
+        "reference_published": {"value": REF_GAME_FPS_RTX5090, "envs": REF_GAME_ENVS,
+                                "hardware": "NVIDIA GeForce RTX 5090",
+                                "source": "src/tests/README.md:142,144-145",
+                                "ratio": fps / REF_GAME_FPS_RTX5090},
+    }
     print(json.dumps(result), flush=True)
 
 
