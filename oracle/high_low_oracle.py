@@ -18,6 +18,16 @@ arrays wrap like torch's int32 kernels), on top of the C market oracle
 * the text renderings ToString (:398-466), InformationStateString (:620-680) and
   PublicInformationString (:682-804), as module functions.
 
+What pins each part (tests/test_high_low_oracle.py; values worked out on paper in
+tests/high_low_cases.py, not by running any implementation): the chance moves, the
+trading move, every reward, portfolio and market row, the returns, one observation
+and ExposeInfo by the hand-derived four-player game; the reward formula also by an
+identity (without penalties a player's rewards over a game sum to its return plus
+|target|*V for a customer); the input checks by a hand case; the text renderings by
+hand-written text; DoReset by replaying the hand game after a reset; the order
+matching underneath by the market oracle's own pins (oracle/market_oracle.c). No function
+here is left unpinned.
+
 The market shape defaults to the game's own (:57-69): L = max_contract_value + 1,
 O = players * steps_per_player * 2, F = min(O, 2 * max_contracts_per_trade),
 C = players; a harness may pass another (L, O, F, C) with C >= players, as the

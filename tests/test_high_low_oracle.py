@@ -91,3 +91,16 @@ def test_oracle_text_renderings():
         assert oracle_information_state_string(o, p, 0) == (
             "********** Private Information **********\n" + priv +
             "******************************************\n\n" + HAND_PUBLIC_TEXT + book)
+
+
+def test_oracle_reset_replays_identically():
+    """DoReset (:375-394) returns to the initial state: the hand game after a reset
+    gives the same rewards, portfolios, market rows, observation and returns."""
+    o = OracleHighLow(**{k: v for k, v in HAND_GAME["params"].items()})
+    first = _play_hand(o)
+    ret = o.fill_returns().copy()
+    o.reset()
+    assert o.move_number == 0 and o.current_player() == -1 and not o.is_terminal()
+    assert not o.market.customer_portfolios.any() and o.market.global_tid == 0
+    assert _play_hand(o) == first
+    assert np.array_equal(o.fill_returns(), ret)
