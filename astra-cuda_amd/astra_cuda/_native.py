@@ -42,7 +42,6 @@ PROTOTYPES = {
     "astra_market_get_tid": (_c_int, [_vp, ctypes.POINTER(_c_i32)]),
     "astra_market_set_tid": (_c_int, [_vp, _c_i32]),
     "astra_market_shape": (_c_int, [_vp] + [ctypes.POINTER(_c_i32)] * 5),
-    "astra_market_bbo_cache": (_c_int, [_vp, ctypes.POINTER(_vp)]),
     "astra_high_low_trade": (_c_int, [_vp, _vp, _vp]),
     "astra_high_low_observation": (_c_int, [_vp, _vp]),
 }

@@ -83,7 +83,7 @@ Layout make_layout(int64_t M, int64_t L, int64_t O, int64_t C) {
   l.next_slot = off;
   off = align_up(off + (size_t)M * 4, 256);
   l.bbo = off;
-  off = align_up(off + (size_t)4 * M * 4, 256);
+  off = align_up(off + (size_t)2 * M * 4, 256);
   l.tob = off;
   off = align_up(off + (size_t)M * 4, 256);
   l.levels = off;
@@ -118,7 +118,7 @@ namespace {
 struct Book {
   uint64_t *masks;            // [2][W][M]: side 0 = bid, 1 = ask
   int32_t *next_slot;         // [M], in [0, O)
-  int32_t *bbo;               // [4][M]: best bid price, size, best ask price, size
+  int32_t *bbo;               // [2][M]: best bid price, best ask price (NULL: empty side)
   uint32_t *tob;              // [M]: head slots of the best levels, bid | ask << 16
   uint16_t *levels;           // [M][L][4] = {bid_head, bid_tail, ask_head, ask_tail}
   uint4 *records;             // [M][O] = {size, customer, tid, price | next << 16}
@@ -559,13 +559,13 @@ struct StagedBook {
 //
 // A lane waits on memory round trips, so the prologue takes two. The first
 // reads the market's coalesced words: quotes, masks, ring position, and the
-// head slots and head sizes of the best levels as the last call left them
-// (tob, BBO cache). That fixes the best levels after the inserts and whether
-// the book crosses. The second reads the two insert levels' words and, for a
-// market that crosses, the two head records and the next level of each side,
-// all at once, before the inserts write anything; the values are then patched
-// for what the inserts wrote (a slot the ring reuses, a tail link), so the
-// first loop pass starts with everything in registers.
+// head slots of the best levels as the last call left them (tob). That fixes
+// the best levels after the inserts and whether the book crosses. The second
+// reads the two insert levels' words and, for a market that crosses (or whose
+// head sizes the call hands out), the two head records and the next level of
+// each side, all at once, before the inserts write anything; the values are
+// then patched for what the inserts wrote (a slot the ring reuses, a tail
+// link), so the first loop pass starts with everything in registers.
 template <int W, bool GAME, bool CARRY = false>
 ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, MarketCtx &c,
                              LoopState<W> &s, const Carry<W> *cy = nullptr) {
@@ -604,9 +604,14 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
     ask_sz = in.ask_sz[m];
     cust = in.cust[m];
   }
-  int32_t ns, bsz0, asz0;
+  // The head sizes of the best levels (for the BBO of a book that does not
+  // cross) are only wanted where the call returns the BBO itself (the game
+  // move, a multi-step launch); get_bbos reads them from the book otherwise.
+  constexpr bool kSizes = GAME || CARRY;
+  int32_t ns, bsz0 = 0, asz0 = 0;
   uint32_t tob;
-  if (CARRY && Carry<W>::kState && cy->state) {
+  const bool carried = CARRY && Carry<W>::kState && cy->state;
+  if (carried) {
 #pragma unroll
     for (int i = 0; i < W; ++i) {
       s.bm[i] = cy->bm[i];
@@ -624,8 +629,6 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
     }
     ns = b.next_slot[m];
     tob = b.tob[m];
-    bsz0 = b.bbo[M + m];
-    asz0 = b.bbo[3 * M + m];
   }
   c.abort = GAME && in.game.abort_on_error && *in.game.errors != 0;
   if (GAME && c.abort) return;  // nothing written yet
@@ -648,8 +651,9 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   const uint32_t bword = bid_ok ? level_word(lv, bid_px, 0) : 0u;
   const uint32_t aword = ask_ok ? level_word(lv, ask_px, 1) : 0u;
   uint4 hrb = make_uint4((uint32_t)bsz0, 0, 0, 0), hra = make_uint4((uint32_t)asz0, 0, 0, 0);
-  if (cross && !bid_top && hb0 < (uint32_t)O) hrb = rec[hb0];
-  if (cross && !ask_top && ha0 < (uint32_t)O) hra = rec[ha0];
+  const bool head_recs = cross || (kSizes && !carried);
+  if (head_recs && !bid_top && hb0 < (uint32_t)O) hrb = rec[hb0];
+  if (head_recs && !ask_top && ha0 < (uint32_t)O) hra = rec[ha0];
   int pb = -1, pa = L;
   uint32_t pbh = kNull16, pah = kNull16;
   if (cross) {
@@ -723,8 +727,9 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   c.ask_ok = ask_ok;
 
   // ---- the matching loop's entry state ----
-  // For a market that does not cross only the head sizes are used (by the
-  // BBO); they come from the BBO cache unless an insert rewrote the slot.
+  // For a market that does not cross only the head sizes are used, where the
+  // call hands out the BBO; they come from the head records read above (or
+  // the carry) unless an insert rewrote the slot.
   s.bb = bb;
   s.ba = ba;
   s.bh = s.ah = kNull16;
@@ -945,9 +950,9 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
 }
 
 // The end of a market's call: remaining fill rows, fill count, masks, ring
-// position, and the best bid/offer of the book as left (what get_bbo_kernel,
-// market.cu:280-320, would read) into the workspace's BBO cache. STATS also
-// adds the call's work counts.
+// position, and the best levels of the book as left (prices into the
+// workspace's BBO cache, head slots into tob: what get_bbo_kernel,
+// market.cu:280-320, would find). STATS also adds the call's work counts.
 template <int W, bool STATS, bool GAME, bool MULTI, class BookMem>
 ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx &c,
                              const LoopState<W> &s, FillSink &sink, const BookMem &bk,
@@ -958,9 +963,12 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
   // Loads first, then plain stores and the fill rows with their portfolio
   // atomics, then the stores that need the loaded values: the wait for a load
   // also waits for every memory operation issued before it.
+  // The head sizes (GetBBOs' sizes) only where this call hands out the BBO:
+  // loading them ends a chain with one more round trip.
+  constexpr bool kSizes = GAME || MULTI;
   int32_t obs = 0, oas = 0;
-  if (s.bb >= 0 && s.bh < (uint32_t)O) obs = s.have_b ? (int32_t)s.brec.x : bk.size(s.bh);
-  if (s.ba < L && s.ah < (uint32_t)O) oas = s.have_a ? (int32_t)s.arec.x : bk.size(s.ah);
+  if (kSizes && s.bb >= 0 && s.bh < (uint32_t)O) obs = s.have_b ? (int32_t)s.brec.x : bk.size(s.bh);
+  if (kSizes && s.ba < L && s.ah < (uint32_t)O) oas = s.have_a ? (int32_t)s.arec.x : bk.size(s.ah);
   out.counts[m] = s.fc;
   // (a multi-step launch keeps these in registers and stores them after its
   // last step only)
@@ -979,9 +987,7 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
   const uint32_t tob = ((s.bb >= 0 ? s.bh : kNull16) & kNull16) | ((s.ba < L ? s.ah : kNull16) << 16);
   if (store) {
     b.bbo[m] = obp;
-    b.bbo[M + m] = obs;
-    b.bbo[2 * M + m] = oap;
-    b.bbo[3 * M + m] = oas;
+    b.bbo[M + m] = oap;
     b.tob[m] = tob;
   }
   if (MULTI && Carry<W>::kState && cy) {
@@ -1027,10 +1033,13 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
 ASTRA_HD void bbo_copy_market(const Book &b, int32_t *bid_px, int32_t *bid_sz, int32_t *ask_px,
                               int32_t *ask_sz, int64_t m) {
   const int64_t M = b.M;
-  bid_px[m] = b.bbo[m];
-  bid_sz[m] = b.bbo[M + m];
-  ask_px[m] = b.bbo[2 * M + m];
-  ask_sz[m] = b.bbo[3 * M + m];
+  const int32_t bp = b.bbo[m], ap = b.bbo[M + m];
+  const uint32_t t = b.tob[m], bh = t & kNull16, ah = t >> 16;
+  const uint4 *rec = b.records + m * (int64_t)b.O;
+  bid_px[m] = bp;
+  ask_px[m] = ap;
+  bid_sz[m] = (bp != ASTRA_NULL_INDEX && bh < (uint32_t)b.O) ? (int32_t)rec[bh].x : 0;
+  ask_sz[m] = (ap != ASTRA_NULL_INDEX && ah < (uint32_t)b.O) ? (int32_t)rec[ah].x : 0;
 }
 
 // update_last_prices_kernel (market.cu:767-786). A count above F (only possible
@@ -1061,9 +1070,7 @@ ASTRA_HD void clear_quotes_thread(const Book &b, const uint8_t *reset, int64_t t
     for (int i = 0; i < 2 * W; ++i) b.masks[(int64_t)i * M + m] = 0ull;
     b.next_slot[m] = 0;
     b.bbo[m] = ASTRA_NULL_INDEX;
-    b.bbo[M + m] = 0;
-    b.bbo[2 * M + m] = ASTRA_NULL_INDEX;
-    b.bbo[3 * M + m] = 0;
+    b.bbo[M + m] = ASTRA_NULL_INDEX;
     b.tob[m] = 0xFFFFFFFFu;
   }
 }
@@ -1473,12 +1480,9 @@ int init_book(astra_market *h, hipStream_t s) {
   int rc;
   if ((rc = launch_fill(h->ws + l.masks, (int64_t)(l.bbo - l.masks) / 4, 0u, s, "init")))
     return rc;
-  // BBO cache of an empty book: (NULL, 0, NULL, 0)
+  // BBO cache of an empty book: both prices NULL
   int32_t *bbo = reinterpret_cast<int32_t *>(h->ws + l.bbo);
-  if ((rc = launch_fill(bbo, h->M, 0xFFFFFFFFu, s, "init"))) return rc;
-  if ((rc = launch_fill(bbo + h->M, h->M, 0u, s, "init"))) return rc;
-  if ((rc = launch_fill(bbo + 2 * (int64_t)h->M, h->M, 0xFFFFFFFFu, s, "init"))) return rc;
-  if ((rc = launch_fill(bbo + 3 * (int64_t)h->M, h->M, 0u, s, "init"))) return rc;
+  if ((rc = launch_fill(bbo, 2 * (int64_t)h->M, 0xFFFFFFFFu, s, "init"))) return rc;
   if ((rc = launch_fill(h->ws + l.tob, h->M, 0xFFFFFFFFu, s, "init"))) return rc;
   if ((rc = launch_fill(h->ws + l.levels, (int64_t)h->M * h->L * 2, 0xFFFFFFFFu, s, "init")))
     return rc;
@@ -1842,12 +1846,6 @@ int astra_market_shape(const astra_market *h, int32_t *M, int32_t *L, int32_t *O
   if (O) *O = h->O;
   if (F) *F = h->F;
   if (C) *C = h->C;
-  return ASTRA_OK;
-}
-
-int astra_market_bbo_cache(const astra_market *h, int32_t **bbo) {
-  if (!h || !bbo) return fail(ASTRA_ERR_INVALID_ARGUMENT, "astra_market_bbo_cache: null argument");
-  *bbo = reinterpret_cast<int32_t *>(h->ws + h->lay.bbo);
   return ASTRA_OK;
 }
 

@@ -129,8 +129,10 @@ int astra_market_add_two_sided_quotes_steps(
     int32_t *step_fill_counts, int32_t *step_bbos, void *stream);
 
 /* VecMarket::GetBBOs (market.cu:573-597): four int32 [M] outputs. The values
- * are those of the book as the last mutating call left it (the matching kernel
- * computes them; this call copies them out). */
+ * are those of the book as the last mutating call left it: the matching kernel
+ * leaves the best levels' prices and head slots, and this call reads the head
+ * orders' sizes from the book (get_bbo_kernel, market.cu:280-320, scans for the
+ * same levels and reads the same sizes). */
 int astra_market_get_bbos(const astra_market *market, int32_t *best_bid_prices,
                           int32_t *best_bid_sizes, int32_t *best_ask_prices,
                           int32_t *best_ask_sizes, void *stream);
@@ -167,12 +169,6 @@ int astra_market_portfolios(const astra_market *market, int32_t **portfolios);
 int astra_market_shape(const astra_market *market, int32_t *num_markets, int32_t *max_price_levels,
                        int32_t *max_active_orders_per_market, int32_t *max_active_fills_per_market,
                        int32_t *num_customers);
-
-/* Device address of the BBO the last mutating call left: int32 [4, M] = best bid
- * prices, best bid sizes, best ask prices, best ask sizes (what
- * astra_market_get_bbos copies out; get_bbo_kernel, market.cu:280-320, computes
- * the same values). For kernels that consume the BBO directly. */
-int astra_market_bbo_cache(const astra_market *market, int32_t **bbo);
 
 /* VecMarket::ToString (market.cu:599-691). Synchronises `stream`, formats the
  * book of market_id into buf (NUL-terminated, truncated to buflen) and stores

@@ -31,7 +31,7 @@ def test_header_declares_entry_points():
     for must in ("astra_market_create", "astra_market_add_two_sided_quotes", "astra_market_get_bbos",
                  "astra_update_last_prices", "astra_market_reset", "astra_market_clear_quotes",
                  "astra_market_clone", "astra_market_to_string", "astra_market_portfolios",
-                 "astra_market_shape", "astra_market_bbo_cache", "astra_high_low_trade",
+                 "astra_market_shape", "astra_high_low_trade",
                  "astra_high_low_observation"):
         assert must in names
 
