@@ -9,13 +9,34 @@ import pytest
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "golden"))
-from make_config1_digest import BBO, FIELDS, run, step_digest  # noqa: E402
+from make_config1_digest import BBO, DUMP_STEPS, FIELDS, run, step_digest, step_dump  # noqa: E402
 
 GOLDEN = json.load(open(os.path.join(HERE, "golden", "config1_digest.json")))["steps"]
+DUMPS = {d["step"]: d for d in json.load(open(os.path.join(HERE, "golden", "config1_dumps.json")))["dumps"]}
 
 
 def test_oracle_reproduces_config1_digest():
-    assert run() == GOLDEN
+    dumps = []
+    assert run(dumps=dumps) == GOLDEN
+    assert sorted(DUMPS) == list(DUMP_STEPS)
+    for d in dumps:
+        assert d == DUMPS[d["step"]], d["step"]
+
+
+def test_config1_dumps_match_their_digests():
+    """The full dumps and the digests were written from the same run."""
+    from astra_cuda.workloads import CONFIGS
+    F = CONFIGS[1].F
+    for t, d in DUMPS.items():
+        counts = np.array(d["fill_counts"], np.int32)
+        M = counts.shape[0]
+        fills = {f: np.zeros((M, F), np.int32) for f in FIELDS}
+        for m, rows in d["rows"].items():
+            r = np.array(rows, np.int32)
+            for i, f in enumerate(FIELDS):
+                fills[f][int(m), :len(r)] = r[:, i]
+        bbo = {f: np.array(v, np.int32) for f, v in d["bbo"].items()}
+        assert step_digest(counts, fills, bbo, np.array(d["portfolios"], np.int32), F) == GOLDEN[t], t
 
 
 def _drive(mk, fills, bbo, arrays, steps=None):
@@ -28,6 +49,10 @@ def _drive(mk, fills, bbo, arrays, steps=None):
         arrays["after"]()
         f, b, pf = arrays["read"]()
         out.append(step_digest(f["fill_counts"], f, b, pf, cfg.F))
+        if t in DUMPS:  # in full, so a mismatch names its field and market
+            d = step_dump(t, f["fill_counts"], f, b, pf, cfg.F)
+            for key in ("fill_counts", "rows", "bbo", "portfolios"):
+                assert d[key] == DUMPS[t][key], (t, key)
         if out[-1] != GOLDEN[t]:
             raise AssertionError(f"step {t}: digest {out[-1]} != golden {GOLDEN[t]}")
     return out
