@@ -136,6 +136,24 @@ def test_gpu_markets_per_wavefront(per_wave, stage_budget):
     assert r["fill_rows"] > 0
 
 
+def test_gpu_max_markets():
+    """The reference's market cap, 2048 * 2048 = 4,194,304 markets (market.h:56), on a
+    small book: launch geometry and 64-bit indexing at the largest grid, every output
+    compared in full with the oracle over a few steps (eviction and overflow included)."""
+    from astra_cuda import order_matching as aom
+    M, L, O, F, C, steps = aom.MAX_MARKETS, 8, 2, 3, 4, 4
+    _log(f"max markets M={M}")
+    rng = np.random.default_rng(7)
+
+    def gen(t):
+        return (rng.integers(0, L, M).astype(np.int32), rng.integers(0, 6, M).astype(np.int32),
+                rng.integers(0, L, M).astype(np.int32), rng.integers(0, 6, M).astype(np.int32),
+                rng.integers(0, C, M).astype(np.int32))
+
+    r = run_parity(M, L, O, F, C, steps, gen, full_every=1, label="max markets")
+    assert r["fill_rows"] > 0 and r["overflows"] > 0
+
+
 def test_gpu_reset_clear_clone_and_to_string():
     """Reset / ClearQuotes / copy constructor / ToString interleaved with trading."""
     from astra_cuda import order_matching as aom
