@@ -228,21 +228,29 @@ def main():
     # ---- S: the same K steps as ONE multi-step launch (every step's BBOs kept) ----
     multistep = None
     if "S" in phases:
-        sfills = snaps[4].new_fill_batch()
         step_bbos = torch.empty((4, K, M), dtype=torch.int32, device=dev) if bbo else None
         ins = [x[W:T] for x in dev_in]
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        torch.cuda.synchronize()
-        s0 = time.perf_counter()
-        ev[0].record()
-        snaps[4].add_two_sided_quotes_steps(*ins, sfills, step_bbos=step_bbos)
-        ev[1].record()
-        torch.cuda.synchronize()
-        wall_ms = time.perf_counter() - s0
+
+        def one_launch(mk, layout):
+            sfills = mk.new_fill_batch(layout)
+            torch.cuda.synchronize()
+            s0 = time.perf_counter()
+            ev[0].record()
+            mk.add_two_sided_quotes_steps(*ins, sfills, step_bbos=step_bbos)
+            ev[1].record()
+            torch.cuda.synchronize()
+            return time.perf_counter() - s0, ev[0].elapsed_time(ev[1]) / K
+
+        mk_rows = snaps[4].clone()
+        wall_ms, dev_ms = one_launch(snaps[4], "columns")
+        wall_ms_rows, _ = one_launch(mk_rows, "rows")
+        del mk_rows
         multistep = {"value": M * K / wall_ms, "ms_per_step": wall_ms / K * 1e3,
-                     "device_ms_per_step": ev[0].elapsed_time(ev[1]) / K, "steps_per_launch": K,
+                     "device_ms_per_step": dev_ms, "steps_per_launch": K,
+                     "value_rows_layout": M * K / wall_ms_rows,
                      "kernel": "quote_match_kernel (multi-step)"}
-        log(f"S: {K} steps in one launch, {wall_ms * 1e3:.2f} ms")
+        log(f"S: {K} steps in one launch, {wall_ms * 1e3:.2f} ms ({wall_ms_rows * 1e3:.2f} ms with rows)")
     log(f"work over {K} steps: inserts {n_ins}, fill rows {n_fill}, emptied {n_empty}, overflow {n_ovf}")
 
     # algorithmic bytes (per launch of the matching kernel): quotes in 20 B + fill_counts 4 B
