@@ -15,10 +15,21 @@ def _t(a):
     return torch.as_tensor(np.ascontiguousarray(a)).to(DEV)
 
 
-def _game(params):
+def _game(params, stage_budget=None):
+    import os
     import astra_cuda as astra
     astra.register_games()
-    return astra.load_game("high_low_trading", params)
+    old = os.environ.get("ASTRA_MARKET_STAGE_BUDGET")
+    if stage_budget is not None:  # read when the game's market is created
+        os.environ["ASTRA_MARKET_STAGE_BUDGET"] = str(stage_budget)
+    try:
+        return astra.load_game("high_low_trading", params)
+    finally:
+        if stage_budget is not None:
+            if old is None:
+                del os.environ["ASTRA_MARKET_STAGE_BUDGET"]
+            else:
+                os.environ["ASTRA_MARKET_STAGE_BUDGET"] = old
 
 
 def _compare(o, s, where):
@@ -47,16 +58,19 @@ def _params(N, P, T, S, cM, V, shape):
     return p
 
 
-@pytest.mark.parametrize("N,P,T,S,cM,V,shape,seed", [
-    (500, 5, 4, 5, 5, 30, None, 1),
-    (300, 4, 6, 3, 4, 20, (21, 12, 6, 4), 2),         # ring of 12: slot reuse
-    (2000, 5, 3, 5, 5, 127, (128, 1024, 10, 16), 3),  # the config-5 shape
+@pytest.mark.parametrize("N,P,T,S,cM,V,shape,seed,budget", [
+    (500, 5, 4, 5, 5, 30, None, 1, None),
+    (300, 4, 6, 3, 4, 20, (21, 12, 6, 4), 2, None),         # ring of 12: slot reuse
+    (2000, 5, 3, 5, 5, 127, (128, 1024, 10, 16), 3, None),  # the config-5 shape
+    (300, 8, 3, 5, 5, 30, None, 4, 1),     # 8 and 9 players, staging forced
+    (300, 9, 3, 5, 5, 30, None, 5, 1),
+    (300, 5, 8, 3, 4, 20, (21, 12, 6, 5), 6, 1),
 ])
-def test_gpu_game_vs_oracle(N, P, T, S, cM, V, shape, seed):
-    print(f"game N={N} P={P} T={T} shape={shape}", flush=True)
+def test_gpu_game_vs_oracle(N, P, T, S, cM, V, shape, seed, budget):
+    print(f"game N={N} P={P} T={T} shape={shape} stage budget {budget}", flush=True)
     rng = np.random.default_rng(seed)
     o = OracleHighLow(N, P, T, S, cM, V, market_shape=shape)
-    g = _game(_params(N, P, T, S, cM, V, shape))
+    g = _game(_params(N, P, T, S, cM, V, shape), budget)
     s = g.new_initial_state()
     chance, moves = random_game(rng, N, P, T, S, cM, V)
     for c in chance:

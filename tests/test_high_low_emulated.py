@@ -29,10 +29,21 @@ def _compare(o, e, where):
     assert np.array_equal(o.fills.fill_counts, e.fills.fill_counts), where
 
 
-def _play(N, P, T, S, cM, V, shape, seed, obs_every=3, layout="columns"):
+def _play(N, P, T, S, cM, V, shape, seed, obs_every=3, layout="columns", stage_budget=None):
+    import os
     rng = np.random.default_rng(seed)
     o = OracleHighLow(N, P, T, S, cM, V, market_shape=shape)
-    e = EmuHighLow(N, P, T, S, cM, V, (o.L, o.O, o.F, o.C), layout)
+    old = os.environ.get("ASTRA_MARKET_STAGE_BUDGET")
+    if stage_budget is not None:  # read when the market is created
+        os.environ["ASTRA_MARKET_STAGE_BUDGET"] = str(stage_budget)
+    try:
+        e = EmuHighLow(N, P, T, S, cM, V, (o.L, o.O, o.F, o.C), layout)
+    finally:
+        if stage_budget is not None:
+            if old is None:
+                del os.environ["ASTRA_MARKET_STAGE_BUDGET"]
+            else:
+                os.environ["ASTRA_MARKET_STAGE_BUDGET"] = old
     chance, moves = random_game(rng, N, P, T, S, cM, V)
     for c in chance:
         o.apply_action(c)
@@ -57,6 +68,17 @@ def _play(N, P, T, S, cM, V, shape, seed, obs_every=3, layout="columns"):
 @pytest.mark.parametrize("layout", ["columns", "rows"])
 def test_emulated_game_vs_oracle(N, P, T, S, cM, V, shape, seed, layout):
     _play(N, P, T, S, cM, V, shape, seed, layout=layout)
+
+
+@pytest.mark.parametrize("N,P,T,S,cM,V,shape,seed", [
+    (40, 8, 3, 5, 5, 30, None, 5),     # 8 and 9 players
+    (40, 9, 3, 5, 5, 30, None, 6),
+    (50, 5, 8, 3, 4, 20, (21, 12, 6, 5), 7),
+])
+def test_emulated_game_staged_and_player_counts(N, P, T, S, cM, V, shape, seed):
+    """Every market that crosses twice finished from its staged book (stage budget 1),
+    with more players than the default games have."""
+    _play(N, P, T, S, cM, V, shape, seed, layout="rows", stage_budget=1)
 
 
 def test_emulated_hand_game():
