@@ -63,43 +63,8 @@ ASTRA_HD int32_t load_past_l1(const int32_t *p) {
 #endif
 }
 
-// Env m's players' portfolios during one move, in registers (up to kMax
-// players): the snapshot before the move and the snapshot plus the changes of
-// each fill row as the row is produced (the same changes the row's atomic adds
-// make, market.cu:221-232), so the rewards need no second read of the
-// portfolios after the atomics.
-struct GameDelta {
-  static constexpr int kMax = 8;
-  int32_t l_con[kMax], l_cash[kMax];  // before the move
-  uint32_t con[kMax], cash[kMax];     // after the rows so far
-  int32_t C;
-  bool on;  // the env has at most kMax players
-  ASTRA_HD void add(const int32_t (&row)[8]) {
-    const int32_t price = row[0], qty = row[1], taker = row[2], quoter = row[3];
-    const bool ask_quotes = row[4] != 0;
-    const int32_t buyer = ask_quotes ? taker : quoter, seller = ask_quotes ? quoter : taker;
-    if (qty == 0 || (uint32_t)buyer >= (uint32_t)C || (uint32_t)seller >= (uint32_t)C ||
-        buyer == seller)
-      return;
-    const uint32_t notional = (uint32_t)price * (uint32_t)qty;
-#pragma unroll
-    for (int q = 0; q < kMax; ++q) {
-      if (q == buyer) {
-        con[q] += (uint32_t)qty;
-        cash[q] -= notional;
-      }
-      if (q == seller) {
-        con[q] -= (uint32_t)qty;
-        cash[q] += notional;
-      }
-    }
-  }
-};
-
-// Before the matching: checks and the portfolio snapshot of env m (C: the
-// market's customer count).
-ASTRA_HD void game_before(const GameMove &g, const int32_t *pf_m, int64_t m, int32_t bad, int32_t C,
-                          GameDelta &gd) {
+// Before the matching: checks and the portfolio snapshot of env m.
+ASTRA_HD void game_before(const GameMove &g, const int32_t *pf_m, int64_t m, int32_t bad) {
   if (bad) {
 #if defined(__HIP_DEVICE_COMPILE__)
     atomicOr(g.errors, bad);
@@ -107,27 +72,9 @@ ASTRA_HD void game_before(const GameMove &g, const int32_t *pf_m, int64_t m, int
     *g.errors |= bad;
 #endif
   }
-  const int32_t P = g.P;
-  gd.C = C;
-  gd.on = P <= GameDelta::kMax;
-  if (gd.on) {
-#pragma unroll
-    for (int q = 0; q < GameDelta::kMax; ++q) {
-      if (q < P) {
-        const int32_t con = pf_m[q * 2], cash = pf_m[q * 2 + 1];
-        g.last_pos[(m * P + q) * 2] = con;
-        g.last_pos[(m * P + q) * 2 + 1] = cash;
-        gd.l_con[q] = con;
-        gd.l_cash[q] = cash;
-        gd.con[q] = (uint32_t)con;
-        gd.cash[q] = (uint32_t)cash;
-      }
-    }
-    return;
-  }
-  for (int32_t p = 0; p < P; ++p) {
-    g.last_pos[(m * P + p) * 2] = pf_m[p * 2];
-    g.last_pos[(m * P + p) * 2 + 1] = pf_m[p * 2 + 1];
+  for (int32_t p = 0; p < g.P; ++p) {
+    g.last_pos[(m * g.P + p) * 2] = pf_m[p * 2];
+    g.last_pos[(m * g.P + p) * 2 + 1] = pf_m[p * 2 + 1];
   }
 }
 
@@ -135,8 +82,7 @@ ASTRA_HD void game_before(const GameMove &g, const int32_t *pf_m, int64_t m, int
 // price, telemetry and rewards of env m. fills = this call's fill count,
 // last_px = the price of its last fill row.
 ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *pf_m, int64_t m,
-                         const int32_t (&bbo)[4], int32_t fills, int32_t last_px,
-                         const GameDelta &gd) {
+                         const int32_t (&bbo)[4], int32_t fills, int32_t last_px) {
   for (int k = 0; k < 4; ++k) g.bbo_out[k][m] = bbo[k];
   int32_t last = g.last_prices[m];
   if (fills > 0) {  // UpdateLastPrices (market.cu:767-786)
@@ -161,7 +107,12 @@ ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *p
   const int32_t ask_cheap = (q.ask_sz == 0 && q.ask_px != V) ? V : 0;          // :315
   const bool settle = tmn == T * P - 1;                                         // :319
   const int32_t value = g.contract_values[m * 3 + 2];
-  auto reward = [&](int32_t p, int32_t c_con, int32_t c_cash, int32_t l_con, int32_t l_cash) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_s_waitcnt(0);  // this lane's portfolio atomics have reached L2
+#endif
+  for (int32_t p = 0; p < P; ++p) {
+    const int32_t c_con = load_past_l1(pf_m + p * 2), c_cash = load_past_l1(pf_m + p * 2 + 1);
+    const int32_t l_con = g.last_pos[(m * P + p) * 2], l_cash = g.last_pos[(m * P + p) * 2 + 1];
     const int32_t tgt = g.target[m * P + p];
     pc[((int64_t)p * T + pmn) * 6 + 4] = c_con;
     pc[((int64_t)p * T + pmn) * 6 + 5] = c_cash;
@@ -172,19 +123,7 @@ ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *p
     g.imm[m * P + p] = r;
     const int32_t before = p == player ? 0 : g.rsla[m * P + p];  // :277
     g.rsla[m * P + p] = g_add(before, r);
-  };
-  if (gd.on) {
-#pragma unroll
-    for (int p = 0; p < GameDelta::kMax; ++p)
-      if (p < P) reward(p, (int32_t)gd.con[p], (int32_t)gd.cash[p], gd.l_con[p], gd.l_cash[p]);
-    return;
   }
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_s_waitcnt(0);  // this lane's portfolio atomics have reached L2
-#endif
-  for (int32_t p = 0; p < P; ++p)
-    reward(p, load_past_l1(pf_m + p * 2), load_past_l1(pf_m + p * 2 + 1),
-           g.last_pos[(m * P + p) * 2], g.last_pos[(m * P + p) * 2 + 1]);
 }
 
 // One fused trading move of every env of `market` (implemented with the matching

@@ -363,7 +363,6 @@ struct FillSink {
 #endif
   int64_t base = 0;  // fill index of buffered row 0
   int32_t n = 0;     // rows buffered
-  GameDelta *gd = nullptr;  // the game move's register copy of the portfolios, or null
 
   ASTRA_HD void flush(const FillOut &out, int32_t *pf, int32_t C) {
     if (n == 0) return;
@@ -423,7 +422,6 @@ struct FillSink {
   ASTRA_HD void put(const FillOut &out, int32_t *pf, int32_t C, const int32_t (&row)[8]) {
 #pragma unroll
     for (int f = 0; f < 8; ++f) at(f, n) = row[f];
-    if (gd && gd->on) gd->add(row);
     if (++n == kRows) flush(out, pf, C);
   }
 };
@@ -438,12 +436,10 @@ struct RowBuffer {
   int32_t cap;
   int32_t n;
   int64_t base;  // fill index of row 0
-  GameDelta *gd = nullptr;  // as in FillSink
   ASTRA_HD bool full() const { return n == cap; }
   ASTRA_HD void put(const FillOut &, int32_t *, int32_t, const int32_t (&row)[8]) {
 #pragma unroll
     for (int f = 0; f < 8; ++f) rows[n * 8 + f] = row[f];
-    if (gd && gd->on) gd->add(row);
     ++n;
   }
 };
@@ -472,7 +468,6 @@ struct MarketCtx {
   bool bid_ok, ask_ok;
   GameQuote gq;           // the game's move (GAME only)
   bool abort;             // GAME: a failed check stops the whole move
-  GameDelta gd;           // GAME: the env's players' portfolios during the move
 };
 
 // The matching loop's state: everything a lane needs to resume the loop later.
@@ -637,7 +632,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   }
   c.abort = GAME && in.game.abort_on_error && *in.game.errors != 0;
   if (GAME && c.abort) return;  // nothing written yet
-  if (GAME) game_before(in.game, c.pf, m, c.gq.bad, b.C, c.gd);
+  if (GAME) game_before(in.game, c.pf, m, c.gq.bad);
 
   const bool bid_ok = bid_sz > 0 && (uint32_t)bid_px < (uint32_t)L;
   const bool ask_ok = ask_sz > 0 && (uint32_t)ask_px < (uint32_t)L;
@@ -1009,7 +1004,7 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
   }
   if (GAME) {
     const int32_t bbo[4] = {obp, obs, oap, oas};
-    game_after(game, c.gq, c.pf, m, bbo, s.fc, s.last_px, c.gd);
+    game_after(game, c.gq, c.pf, m, bbo, s.fc, s.last_px);
   }
   if (MULTI) {
     if (so.counts) so.counts[m] = s.fc;
@@ -1178,7 +1173,6 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     if (MULTI && m < b.M) load_next_quotes(in, b.M, k + 1, steps, m, cy);
     if (m < b.M && !(GAME && c.abort)) {
       sink.base = m * (int64_t)b.F;
-      if (GAME) sink.gd = &c.gd;
       const GlobalBook gb{c.lv, c.rec};
       if (match_loop<W, STATS>(st, c, gb, sink, out, bulk, budget)) {
         quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, gb, ink.game, sok, &cy, last);
@@ -1221,7 +1215,6 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
       const StagedBook sb{reinterpret_cast<uint16_t *>(slv), srec};
       RowBuffer rb{rows, kStageRows, 0, 0};
       if (lane == src) rb.base = sink.base;
-      if (GAME && lane == src) rb.gd = &c.gd;
       // The owning lane runs until its market is done or its row buffer is
       // full; then all 64 lanes write the rows out, coalesced.
       bool done = false;
@@ -1343,7 +1336,6 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
       if (MULTI) load_next_quotes(in, b.M, k + 1, steps, m, *cy);
       if (GAME && c.abort) continue;
       sink.base = m * (int64_t)b.F;
-      if (GAME) sink.gd = &c.gd;
       const GlobalBook gb{c.lv, c.rec};
       const bool done = b.stats ? match_loop<W, true>(st, c, gb, sink, fo, bulk, budget)
                                 : match_loop<W, false>(st, c, gb, sink, fo, bulk, budget);
@@ -1358,7 +1350,6 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
         std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
         const StagedBook sb{slv.data(), srec.data()};
         RowBuffer rb{rows.data(), kStageRows, 0, sink.base};
-        if (GAME) rb.gd = &c.gd;
         bool fin = false;
         while (!fin) {
           fin = b.stats ? match_loop<W, true>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF)
