@@ -13,6 +13,7 @@ import pytest
 
 from emu_engine import EmuAdapter, EmuMarket, EmuRowAdapter
 from kat_harness import FILL_FIELDS, load_kats, run_scenario
+from quote_gen import EXT_CAP_CASES, drifting_window_gen
 from oracle.oracle import OracleMarket
 
 SCENARIOS = load_kats()
@@ -90,6 +91,7 @@ ALIAS_CASES = [
     (48, 200, 9, 5, 3, 200, 6),
     (48, 512, 6, 8, 70, 200, 7),
     (32, 1000, 11, 9, 3, 200, 8),
+    (64, 128, 7, 16, 1024, 200, 9),  # C = 1024, the reference's customer cap
 ]
 
 
@@ -115,6 +117,15 @@ def test_emulated_aliasing_vs_oracle(M, L, O, F, C, steps, seed, stage_budget, l
     assert st["fast_forwards"] > 0
     if O > 1:
         assert st["overflows"] > st["fast_forwards"]
+
+
+@pytest.mark.parametrize("name,M,L,O,F,C,steps", EXT_CAP_CASES, ids=[c[0] for c in EXT_CAP_CASES])
+def test_emulated_extended_caps(name, M, L, O, F, C, steps):
+    M = min(M, 16)
+    _, om, st = _run(M, L, O, F, C, steps, drifting_window_gen(M, L, C, seed=21), with_stats=True)
+    assert st["fills"] > 0
+    # the slot counter counts every accepted insert (slot = counter % O)
+    assert om.order_next_slots.min() >= (O + 1000 if name == "wrap" else 2)
 
 
 def test_emulated_config1_full_run():

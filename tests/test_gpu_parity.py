@@ -12,6 +12,7 @@ import torch
 from kat_harness import load_kats, run_scenario
 from parity_util import (DEV, GpuAdapter, GpuRowAdapter, compare_bbo, compare_fills, compare_portfolios,
                          run_parity, t32)
+from quote_gen import EXT_CAP_CASES, drifting_window_gen
 
 pytestmark = pytest.mark.gpu
 
@@ -91,6 +92,7 @@ ALIAS_CASES = [
     (200, 200, 9, 5, 3, 300, 16),
     (200, 512, 6, 8, 70, 300, 17),
     (150, 1000, 11, 9, 3, 300, 18),
+    (128, 128, 7, 16, 1024, 300, 19),  # C = 1024, the reference's customer cap
 ]
 
 
@@ -114,6 +116,18 @@ def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, lay
                    stage_budget=stage_budget, layout=layout)
     if O <= 3:
         assert r["overflows"] > 0
+
+
+@pytest.mark.parametrize("name,M,L,O,F,C,steps", EXT_CAP_CASES, ids=[c[0] for c in EXT_CAP_CASES])
+def test_gpu_extended_caps(name, M, L, O, F, C, steps):
+    """The largest extended shape (16 mask words, slot indices up to 32767, 65,536 fill
+    rows and customers), unstaged; "wrap" reuses every ring slot."""
+    _log(f"extended caps {name}: M={M} L={L} O={O} F={F} C={C} x {steps} steps")
+    every = 1 if steps < 1000 else 10
+    r = run_parity(M, L, O, F, C, steps, drifting_window_gen(M, L, C, seed=21), bbo_every=every,
+                   last_every=every, label=f"ext {name}")
+    assert r["fill_rows"] > 0
+    assert r["oracle"].order_next_slots.min() >= (O + 1000 if name == "wrap" else 2)
 
 
 @pytest.mark.parametrize("per_wave,stage_budget", [(1, 1), (7, None), (32, 1), (33, None)])
