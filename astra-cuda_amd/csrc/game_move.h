@@ -63,8 +63,35 @@ ASTRA_HD int32_t load_past_l1(const int32_t *p) {
 #endif
 }
 
-// Before the matching: checks and the portfolio snapshot of env m.
-ASTRA_HD void game_before(const GameMove &g, const int32_t *pf_m, int64_t m, int32_t bad) {
+// Players are handled kPlayerBatch at a time, every load of a batch issued
+// before any of its stores: the compiler cannot tell the arrays apart, so a
+// load placed after a store waits for the store, one round trip per load. The
+// loads are unconditional (a batch slot beyond the last player reads the last
+// player again): a load under a branch is waited for where the branch ends.
+constexpr int32_t kPlayerBatch = 8;
+
+// The portfolios of env m's first kPlayerBatch players, loaded for the
+// snapshot game_before stores; loaded together with the market's first words,
+// so the snapshot takes no round trip of its own.
+struct GameSnap {
+  int32_t con[kPlayerBatch], cash[kPlayerBatch];
+};
+
+ASTRA_HD GameSnap game_snapshot(const GameMove &g, const int32_t *pf_m) {
+  GameSnap s;
+#pragma unroll
+  for (int32_t j = 0; j < kPlayerBatch; ++j) {
+    const int32_t q = j < g.P ? j : g.P - 1;
+    s.con[j] = pf_m[q * 2];
+    s.cash[j] = pf_m[q * 2 + 1];
+  }
+  return s;
+}
+
+// Before the matching: the check bits and the portfolio snapshot
+// (CopyCustomerPortfoliosTo, :257) of env m.
+ASTRA_HD void game_before(const GameMove &g, const GameSnap &snap, const int32_t *pf_m, int64_t m,
+                          int32_t bad) {
   if (bad) {
 #if defined(__HIP_DEVICE_COMPILE__)
     atomicOr(g.errors, bad);
@@ -72,9 +99,29 @@ ASTRA_HD void game_before(const GameMove &g, const int32_t *pf_m, int64_t m, int
     *g.errors |= bad;
 #endif
   }
-  for (int32_t p = 0; p < g.P; ++p) {
-    g.last_pos[(m * g.P + p) * 2] = pf_m[p * 2];
-    g.last_pos[(m * g.P + p) * 2 + 1] = pf_m[p * 2 + 1];
+  int32_t *last = g.last_pos + m * g.P * 2;
+#pragma unroll
+  for (int32_t j = 0; j < kPlayerBatch; ++j) {
+    if (j < g.P) {
+      last[j * 2] = snap.con[j];
+      last[j * 2 + 1] = snap.cash[j];
+    }
+  }
+  for (int32_t p0 = kPlayerBatch; p0 < g.P; p0 += kPlayerBatch) {
+    int32_t con[kPlayerBatch], cash[kPlayerBatch];
+#pragma unroll
+    for (int32_t j = 0; j < kPlayerBatch; ++j) {
+      const int32_t q = p0 + j < g.P ? p0 + j : g.P - 1;
+      con[j] = pf_m[q * 2];
+      cash[j] = pf_m[q * 2 + 1];
+    }
+#pragma unroll
+    for (int32_t j = 0; j < kPlayerBatch; ++j) {
+      if (p0 + j < g.P) {
+        last[(p0 + j) * 2] = con[j];
+        last[(p0 + j) * 2 + 1] = cash[j];
+      }
+    }
   }
 }
 
@@ -110,19 +157,36 @@ ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *p
 #if defined(__HIP_DEVICE_COMPILE__)
   __builtin_amdgcn_s_waitcnt(0);  // this lane's portfolio atomics have reached L2
 #endif
-  for (int32_t p = 0; p < P; ++p) {
-    const int32_t c_con = load_past_l1(pf_m + p * 2), c_cash = load_past_l1(pf_m + p * 2 + 1);
-    const int32_t l_con = g.last_pos[(m * P + p) * 2], l_cash = g.last_pos[(m * P + p) * 2 + 1];
-    const int32_t tgt = g.target[m * P + p];
-    pc[((int64_t)p * T + pmn) * 6 + 4] = c_con;
-    pc[((int64_t)p * T + pmn) * 6 + 5] = c_cash;
-    int32_t r = tgt != 0 ? g_mul(g_sub(g_abs(g_sub(l_con, tgt)), g_abs(g_sub(c_con, tgt))), V) : 0;
-    r = g_add(r, g_sub(c_cash, l_cash));
-    if (p == player) r = g_sub(g_sub(g_sub(r, penalty), bid_cheap), ask_cheap);
-    if (settle) r = g_add(r, g_mul(c_con, value));
-    g.imm[m * P + p] = r;
-    const int32_t before = p == player ? 0 : g.rsla[m * P + p];  // :277
-    g.rsla[m * P + p] = g_add(before, r);
+  for (int32_t p0 = 0; p0 < P; p0 += kPlayerBatch) {
+    int32_t c_con[kPlayerBatch], c_cash[kPlayerBatch], l_con[kPlayerBatch], l_cash[kPlayerBatch];
+    int32_t tgt[kPlayerBatch], since[kPlayerBatch];
+#pragma unroll
+    for (int32_t j = 0; j < kPlayerBatch; ++j) {
+      const int32_t q = p0 + j < P ? p0 + j : P - 1;
+      c_con[j] = load_past_l1(pf_m + q * 2);
+      c_cash[j] = load_past_l1(pf_m + q * 2 + 1);
+      l_con[j] = g.last_pos[(m * P + q) * 2];
+      l_cash[j] = g.last_pos[(m * P + q) * 2 + 1];
+      tgt[j] = g.target[m * P + q];
+      since[j] = g.rsla[m * P + q];
+    }
+#pragma unroll
+    for (int32_t j = 0; j < kPlayerBatch; ++j) {
+      const int32_t p = p0 + j;
+      if (p < P) {
+        pc[((int64_t)p * T + pmn) * 6 + 4] = c_con[j];
+        pc[((int64_t)p * T + pmn) * 6 + 5] = c_cash[j];
+        int32_t r = tgt[j] != 0
+                        ? g_mul(g_sub(g_abs(g_sub(l_con[j], tgt[j])), g_abs(g_sub(c_con[j], tgt[j]))), V)
+                        : 0;
+        r = g_add(r, g_sub(c_cash[j], l_cash[j]));
+        if (p == player) r = g_sub(g_sub(g_sub(r, penalty), bid_cheap), ask_cheap);
+        if (settle) r = g_add(r, g_mul(c_con[j], value));
+        g.imm[m * P + p] = r;
+        const int32_t before = p == player ? 0 : since[j];  // :277
+        g.rsla[m * P + p] = g_add(before, r);
+      }
+    }
   }
 }
 

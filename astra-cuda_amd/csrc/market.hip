@@ -630,9 +630,11 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
     ns = b.next_slot[m];
     tob = b.tob[m];
   }
+  GameSnap snap;
+  if (GAME) snap = game_snapshot(in.game, c.pf);
   c.abort = GAME && in.game.abort_on_error && *in.game.errors != 0;
   if (GAME && c.abort) return;  // nothing written yet
-  if (GAME) game_before(in.game, c.pf, m, c.gq.bad);
+  if (GAME) game_before(in.game, snap, c.pf, m, c.gq.bad);
 
   const bool bid_ok = bid_sz > 0 && (uint32_t)bid_px < (uint32_t)L;
   const bool ask_ok = ask_sz > 0 && (uint32_t)ask_px < (uint32_t)L;
@@ -648,8 +650,13 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   const uint32_t hb0 = tob & kNull16, ha0 = tob >> 16;
 
   // ---- round trip 2 ----
-  const uint32_t bword = bid_ok ? level_word(lv, bid_px, 0) : 0u;
-  const uint32_t aword = ask_ok ? level_word(lv, ask_px, 1) : 0u;
+  // The insert levels' words: unconditional loads (level 0 stands in for a
+  // rejected quote) so that nothing waits on them before the loads below are
+  // issued; conditional ones each cost a round trip of their own.
+  const uint32_t bword_ld = level_word(lv, bid_ok ? bid_px : 0, 0);
+  const uint32_t aword_ld = level_word(lv, ask_ok ? ask_px : 0, 1);
+  const uint32_t bword = bid_ok ? bword_ld : 0u;
+  const uint32_t aword = ask_ok ? aword_ld : 0u;
   uint4 hrb = make_uint4((uint32_t)bsz0, 0, 0, 0), hra = make_uint4((uint32_t)asz0, 0, 0, 0);
   const bool head_recs = cross || (kSizes && !carried);
   if (head_recs && !bid_top && hb0 < (uint32_t)O) hrb = rec[hb0];
