@@ -1043,10 +1043,16 @@ ASTRA_HD void bbo_copy_market(const Book &b, int32_t *bid_px, int32_t *bid_sz, i
   const int32_t bp = b.bbo[m], ap = b.bbo[M + m];
   const uint32_t t = b.tob[m], bh = t & kNull16, ah = t >> 16;
   const uint4 *rec = b.records + m * (int64_t)b.O;
+  // Both head sizes in one round trip: unconditional loads (slot 0 stands in
+  // for a NULL head), issued before any store.
+  const bool bv = bp != ASTRA_NULL_INDEX && bh < (uint32_t)b.O;
+  const bool av = ap != ASTRA_NULL_INDEX && ah < (uint32_t)b.O;
+  const int32_t bs = reinterpret_cast<const int32_t *>(rec + (bv ? bh : 0u))[0];
+  const int32_t as = reinterpret_cast<const int32_t *>(rec + (av ? ah : 0u))[0];
   bid_px[m] = bp;
   ask_px[m] = ap;
-  bid_sz[m] = (bp != ASTRA_NULL_INDEX && bh < (uint32_t)b.O) ? (int32_t)rec[bh].x : 0;
-  ask_sz[m] = (ap != ASTRA_NULL_INDEX && ah < (uint32_t)b.O) ? (int32_t)rec[ah].x : 0;
+  bid_sz[m] = bv ? bs : 0;
+  ask_sz[m] = av ? as : 0;
 }
 
 // update_last_prices_kernel (market.cu:767-786). A count above F (only possible
