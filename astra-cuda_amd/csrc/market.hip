@@ -553,6 +553,77 @@ struct StagedBook {
   ASTRA_HD void set_head(int32_t p, int side, uint32_t h) const { store_head(slv, p, side, h); }
 };
 
+// Wave-uniform copies of the first active lane's values (readfirstlane; the
+// identity on the host). A staged market's loop runs on one lane of its
+// wavefront; on values the compiler knows to be uniform its branches compile to
+// scalar branches instead of exec-mask bookkeeping, which halves the time a
+// pass takes there.
+ASTRA_HD int32_t uni(int32_t v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_readfirstlane(v);
+#else
+  return v;
+#endif
+}
+ASTRA_HD uint32_t uni(uint32_t v) { return (uint32_t)uni((int32_t)v); }
+ASTRA_HD uint64_t uni(uint64_t v) {
+  return (uint64_t)uni((uint32_t)v) | ((uint64_t)uni((uint32_t)(v >> 32)) << 32);
+}
+ASTRA_HD int64_t uni(int64_t v) { return (int64_t)uni((uint64_t)v); }
+ASTRA_HD bool uni(bool v) { return uni((int32_t)(v ? 1 : 0)) != 0; }
+ASTRA_HD uint4 uni(const uint4 &v) { return make_uint4(uni(v.x), uni(v.y), uni(v.z), uni(v.w)); }
+
+// A staged book whose reads are wave-uniform (for the loop run by one lane).
+struct UniformStagedBook : StagedBook {
+  ASTRA_HD uint4 record(uint32_t s) const { return uni(srec[s]); }
+  ASTRA_HD int32_t size(uint32_t s) const {
+    return uni(reinterpret_cast<const int32_t *>(srec + s)[0]);
+  }
+  ASTRA_HD uint32_t word(int32_t p, int side) const { return uni(level_word(slv, p, side)); }
+  ASTRA_HD uint32_t head(int32_t p, int side) const { return uni(level_head(slv, p, side)); }
+};
+
+template <int W>
+ASTRA_HD LoopState<W> uniform_state(const LoopState<W> &a) {
+  LoopState<W> u;
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    u.bm[i] = uni(a.bm[i]);
+    u.am[i] = uni(a.am[i]);
+  }
+  u.bb = uni(a.bb);
+  u.ba = uni(a.ba);
+  u.bh = uni(a.bh);
+  u.ah = uni(a.ah);
+  u.brec = uni(a.brec);
+  u.arec = uni(a.arec);
+  u.have_b = uni(a.have_b);
+  u.have_a = uni(a.have_a);
+  u.pb = uni(a.pb);
+  u.pa = uni(a.pa);
+  u.pbh = uni(a.pbh);
+  u.pah = uni(a.pah);
+  u.ahead = uni(a.ahead);
+  u.fc = uni(a.fc);
+  u.last_px = uni(a.last_px);
+  u.emptied = uni(a.emptied);
+  u.forwarded = uni(a.forwarded);
+  u.npass = uni(a.npass);
+  return u;
+}
+
+// The fields of MarketCtx the matching loop reads, made uniform.
+ASTRA_HD MarketCtx uniform_ctx(const MarketCtx &a) {
+  MarketCtx u = a;
+  u.m = uni(a.m);
+  u.L = uni(a.L);
+  u.O = uni(a.O);
+  u.F = uni(a.F);
+  u.C = uni(a.C);
+  u.ns = uni(a.ns);
+  return u;
+}
+
 // add_orders_kernel (market.cu:17-100) for market m and the set-up of the
 // matching loop (:122-142): masks, the inserts, the heads of the best levels
 // and their records.
@@ -1164,7 +1235,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
   const int lane = (int)(threadIdx.x % 64);
   const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64;
   const int64_t m = lane < per_wave ? wave * per_wave + lane : b.M;
-  int32_t *wave_lds = lds_words + (threadIdx.x / 64) * wave_words;
+  int32_t *wave_lds = lds_words + uni((int32_t)(threadIdx.x / 64) * wave_words);
   FillSink sink;
 #if defined(__HIP_DEVICE_COMPILE__)
   sink.lds = wave_lds;
@@ -1225,15 +1296,25 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const StagedBook sb{reinterpret_cast<uint16_t *>(slv), srec};
+      UniformStagedBook sb;
+      sb.slv = reinterpret_cast<uint16_t *>(slv);
+      sb.srec = srec;
       RowBuffer rb{rows, kStageRows, 0, 0};
       if (lane == src) rb.base = sink.base;
       // The owning lane runs until its market is done or its row buffer is
-      // full; then all 64 lanes write the rows out, coalesced.
+      // full (on uniform copies of its state); then all 64 lanes write the rows
+      // out, coalesced.
       bool done = false;
       while (!done) {
         int32_t fin = 0;
-        if (lane == src) fin = match_loop<W, STATS>(st, c, sb, rb, out, bulk, 0x7FFFFFFF) ? 1 : 0;
+        if (lane == src) {
+          LoopState<W> us = uniform_state(st);
+          const MarketCtx uc = uniform_ctx(c);
+          RowBuffer urb{rows, kStageRows, uni(rb.n), uni(rb.base)};
+          fin = match_loop<W, STATS>(us, uc, sb, urb, out, bulk, 0x7FFFFFFF) ? 1 : 0;
+          st = us;
+          rb.n = urb.n;
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
