@@ -1161,6 +1161,24 @@ ASTRA_HD void clear_quotes_thread(const Book &b, const uint8_t *reset, int64_t t
 
 // ---- __global__ wrappers ----
 
+// A pointer moved into vector registers, opaque to the compiler so that it stays
+// there (the identity on the host). The matching kernel keeps every kernel
+// argument in scalar registers and has more of them live in its loop than
+// there are: the fill-batch pointers (used by the row flushes) go to VGPRs,
+// which the kernel has to spare, instead of being spilled and reloaded around
+// each branch of the loop (-1.5% per step at 100,000 markets, -4.5% at 10,000;
+// not in the game move's kernel, which has no VGPRs to spare).
+template <class T>
+__device__ __forceinline__ T *in_vgpr(T *p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint64_t v = reinterpret_cast<uint64_t>(p);
+  asm volatile("" : "+v"(v));
+  return reinterpret_cast<T *>(v);
+#else
+  return p;
+#endif
+}
+
 // Writes the rows owed by fast-forwarded markets of this wavefront: each such
 // lane's rows are written by all 64 lanes together, coalesced.
 __device__ __forceinline__ void write_bulk_wave(const FillOut &out, const Bulk &bk) {
@@ -1230,6 +1248,18 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
                                                           int32_t budget, int32_t wave_words,
                                                           int32_t per_wave) {
   extern __shared__ int32_t lds_words[];
+  if (!GAME) {
+    out.prices = in_vgpr(out.prices);
+    out.sizes = in_vgpr(out.sizes);
+    out.taker = in_vgpr(out.taker);
+    out.quoter = in_vgpr(out.quoter);
+    out.is_sell_quote = in_vgpr(out.is_sell_quote);
+    out.quote_sizes = in_vgpr(out.quote_sizes);
+    out.tid = in_vgpr(out.tid);
+    out.quote_tid = in_vgpr(out.quote_tid);
+    out.counts = in_vgpr(out.counts);
+    out.rows = in_vgpr(out.rows);
+  }
   // Lanes [0, per_wave) of each wavefront own one market each; the rest idle
   // (and help with the wavefront's cooperative copies).
   const int lane = (int)(threadIdx.x % 64);
