@@ -985,8 +985,11 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
         bk.set_word(s.bb, 0, 0xFFFFFFFFu);
         mask_clear<W>(s.bm, s.bb);
         if (STATS) ++s.emptied;
-        s.bb = mask_highest<W>(s.bm);  // the level read ahead
-        s.bh = s.bb >= 0 ? ((s.bb == s.pb ? s.pbh : bk.word(s.bb, 0)) & kNull16) : kNull16;
+        // the next level is the one read ahead at the top of this pass (pb is
+        // the highest level below bb in the same mask, and only this pop has
+        // changed the mask since)
+        s.bb = s.pb;
+        s.bh = s.bb >= 0 ? (s.pbh & kNull16) : kNull16;
         s.have_b = false;
         s.ahead = false;
       } else if (nh != s.bh) {
@@ -1001,8 +1004,8 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
         bk.set_word(s.ba, 1, 0xFFFFFFFFu);
         mask_clear<W>(s.am, s.ba);
         if (STATS) ++s.emptied;
-        s.ba = mask_lowest<W>(s.am, L);
-        s.ah = s.ba < L ? ((s.ba == s.pa ? s.pah : bk.word(s.ba, 1)) & kNull16) : kNull16;
+        s.ba = s.pa;
+        s.ah = s.ba < L ? (s.pah & kNull16) : kNull16;
         s.have_a = false;
         s.ahead = false;
       } else if (nh != s.ah) {
