@@ -1245,24 +1245,33 @@ ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
 // so each wavefront goes on to its markets' next step as soon as it is done
 // with this one, with no grid-wide wait between steps.
 // All 64 lanes of a wavefront reach the ballots (no early return).
-template <int W, bool STATS, bool GAME, bool MULTI>
+template <int W, bool STATS, bool GAME, bool MULTI, bool ROWS>
 __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, FillOut out,
                                                           StepOut so, int32_t steps,
                                                           int32_t budget, int32_t wave_words,
                                                           int32_t per_wave) {
   extern __shared__ int32_t lds_words[];
-  if (!GAME) {
-    out.prices = in_vgpr(out.prices);
-    out.sizes = in_vgpr(out.sizes);
-    out.taker = in_vgpr(out.taker);
-    out.quoter = in_vgpr(out.quoter);
-    out.is_sell_quote = in_vgpr(out.is_sell_quote);
-    out.quote_sizes = in_vgpr(out.quote_sizes);
-    out.tid = in_vgpr(out.tid);
-    out.quote_tid = in_vgpr(out.quote_tid);
-    out.counts = in_vgpr(out.counts);
-    out.rows = in_vgpr(out.rows);
+  // The FillBatch layout is a template argument: the other layout's pointers
+  // become constant nulls, so their code and registers drop out.
+  if (ROWS) {
+    out.prices = out.sizes = out.taker = out.quoter = nullptr;
+    out.quote_sizes = out.tid = out.quote_tid = nullptr;
+    out.is_sell_quote = nullptr;
+    if (!GAME) out.rows = in_vgpr(out.rows);
+  } else {
+    out.rows = nullptr;
+    if (!GAME) {
+      out.prices = in_vgpr(out.prices);
+      out.sizes = in_vgpr(out.sizes);
+      out.taker = in_vgpr(out.taker);
+      out.quoter = in_vgpr(out.quoter);
+      out.is_sell_quote = in_vgpr(out.is_sell_quote);
+      out.quote_sizes = in_vgpr(out.quote_sizes);
+      out.tid = in_vgpr(out.tid);
+      out.quote_tid = in_vgpr(out.quote_tid);
+    }
   }
+  if (!GAME) out.counts = in_vgpr(out.counts);
   // Lanes [0, per_wave) of each wavefront own one market each; the rest idle
   // (and help with the wavefront's cooperative copies).
   const int lane = (int)(threadIdx.x % 64);
@@ -1503,12 +1512,18 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   const int32_t wave_words = (int32_t)(wave_bytes / 4);
   const int32_t per_wave = markets_per_wave(h, GAME);
   const unsigned grid = grid_for(((int64_t)b.M + per_wave - 1) / per_wave * 64, h->block);
-  if (b.stats)
-    hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI>), dim3(grid), dim3(h->block), lds,
-                       s, b, in, fo, so, steps, budget, wave_words, per_wave);
+  if (b.stats && fo.rows)
+    hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI, true>), dim3(grid), dim3(h->block),
+                       lds, s, b, in, fo, so, steps, budget, wave_words, per_wave);
+  else if (b.stats)
+    hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI, false>), dim3(grid), dim3(h->block),
+                       lds, s, b, in, fo, so, steps, budget, wave_words, per_wave);
+  else if (fo.rows)
+    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, true>), dim3(grid),
+                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words, per_wave);
   else
-    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI>), dim3(grid), dim3(h->block), lds,
-                       s, b, in, fo, so, steps, budget, wave_words, per_wave);
+    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, false>), dim3(grid),
+                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words, per_wave);
 #endif
   ASTRA_HIP_CHECK(rt_last_error(), "AddTwoSidedQuotes");
   return ASTRA_OK;

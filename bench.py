@@ -408,7 +408,7 @@ def bench_game(args):
     traffic, traffic_src = (None, None)
     if N == cfg.envs:
         traffic, traffic_src = profile_traffic(f"game_move_config5_{cfg.name}_kernel_trace.md",
-                                               "quote_match_kernel<2, false, true, false>")
+                                               "quote_match_kernel<2, false, true, false, true>")
     result = {
         "metric": "quote-matches/sec and market-steps/sec at 100k markets; p50 step latency",
         "value": N * K / wall,
@@ -597,7 +597,7 @@ def measured_traffic(cfg, M, bbo):
     while words * 64 < cfg.L:
         words *= 2
     return profile_traffic(f"quote_match_config{cfg.index}_{cfg.name}_hbm_traffic.md",
-                           f"quote_match_kernel<{words}, false, false, false>")
+                           f"quote_match_kernel<{words}, false, false, false, false>")
 
 
 def cpu_baseline(args, cfg, host, M, W, K, bbo):
