@@ -101,6 +101,113 @@ __global__ __launch_bounds__(kBlock) void observation_kernel(astra_hl_observatio
   if (i < total) observation_element(o, i);
 }
 
+// The same observation with one lane per column and a wavefront per
+// kObsEnvsPerWave envs, for rows of at most 64 columns (P <= 8). A column's
+// source is fixed for the call, so every lane loads its column's word of all its
+// envs, and the env's shared words (permutation entry, contract values, settle
+// flag, target) as loads every lane makes alike, before anything waits; the
+// per-element kernel above branches on the column and waits once per branch.
+// Consecutive lanes write consecutive columns of a row.
+constexpr int kObsEnvsPerWave = 16;
+
+// Column j's source (:510-602): kind 0 = one-hot of the permutation entry
+// (j 0-2), 1 = a constant (j 3, 4, 6), 2 = the private information (j 5),
+// 3 = src[n * stride] (the rounds of player_contract_over_time, then the BBO and
+// last-price arrays). Kinds 0-2 read the permutation entry as their word.
+struct ObsColumn {
+  const int32_t *src;
+  int64_t stride;
+  int32_t kind;
+  float constant;
+};
+
+ASTRA_HD ObsColumn obs_column(const astra_hl_observation &o, int32_t j) {
+  const int32_t P = o.players, T = o.steps_per_player, player = o.player, cr = o.current_round;
+  ObsColumn c{o.player_permutation + player, P, 0, 0.0f};
+  if (j <= 2) {
+    c.kind = 0;
+  } else if (j == 3 || j == 4 || j == 6) {
+    c.kind = 1;
+    c.constant = j == 3 ? o.player_sin : j == 4 ? o.player_cos : o.round_fraction;
+  } else if (j == 5) {
+    c.kind = 2;
+  } else if (j < 7 + 6 * P) {  // the round of player p shown to `player` (:559-584)
+    const int32_t q = j - 7, p = q / 6, f = q - 6 * (q / 6);
+    int32_t r;
+    if (cr == 0 || player == P - 1) r = cr;
+    else if (player == 0) r = cr - 1;
+    else r = p < player ? cr : cr - 1;
+    c.src = o.player_contract_over_time + ((int64_t)p * T + r) * 6 + f;
+    c.stride = (int64_t)P * T * 6;
+    c.kind = 3;
+  } else {  // BBO and last price (:589-599)
+    const int32_t k = j - (7 + 6 * P);
+    c.src = k == 0   ? o.best_bid_prices
+            : k == 1 ? o.best_ask_prices
+            : k == 2 ? o.best_bid_sizes
+            : k == 3 ? o.best_ask_sizes
+                     : o.last_prices;
+    c.stride = 1;
+    c.kind = 3;
+  }
+  return c;
+}
+
+// Column j's value for one env from its loaded words (observation_element's
+// cases, in the same order).
+ASTRA_HD float obs_value(const ObsColumn &c, int32_t j, int32_t perm, int32_t word, int32_t cv0,
+                         int32_t cv1, uint8_t settle, int32_t target) {
+  if (c.kind == 0)
+    return (j == 0 ? (perm == 0 || perm == 1) : j == 1 ? perm == 2 : perm > 2) ? 1.0f : 0.0f;
+  if (c.kind == 1) return c.constant;
+  if (c.kind == 2) {
+    if (perm == 0) return (float)cv0;
+    if (perm == 1) return (float)cv1;
+    if (perm == 2) return settle ? 1.0f : 0.0f;
+    if (perm > 2) return (float)target;
+    return 0.0f;
+  }
+  return (float)word;
+}
+
+// Column j of env n (the host build's loop; the kernel below loads the same words).
+ASTRA_HD void observation_column(const astra_hl_observation &o, int64_t n, int32_t j) {
+  const ObsColumn c = obs_column(o, j);
+  const int32_t P = o.players, D = 12 + 6 * P;
+  o.values[n * D + j] =
+      obs_value(c, j, o.player_permutation[n * P + o.player], c.src[n * c.stride],
+                o.contract_values[n * 3], o.contract_values[n * 3 + 1],
+                o.contract_high_settle[n], o.target_positions[n * P + o.player]);
+}
+
+__global__ __launch_bounds__(kBlock) void observation_rows_kernel(astra_hl_observation o,
+                                                                  int64_t N) {
+  const int lane = (int)(threadIdx.x % 64);
+  const int64_t n0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64 * kObsEnvsPerWave;
+  const int32_t P = o.players, player = o.player, D = 12 + 6 * P;
+  const int32_t j = lane < D ? lane : D - 1;  // lanes past the row repeat its last column
+  const ObsColumn c = obs_column(o, j);
+  int32_t perm[kObsEnvsPerWave], word[kObsEnvsPerWave], cv0[kObsEnvsPerWave];
+  int32_t cv1[kObsEnvsPerWave], target[kObsEnvsPerWave];
+  uint8_t settle[kObsEnvsPerWave];
+#pragma unroll
+  for (int e = 0; e < kObsEnvsPerWave; ++e) {  // env index clamped: no branch around a load
+    const int64_t n = n0 + e < N ? n0 + e : N - 1;
+    perm[e] = o.player_permutation[n * P + player];
+    word[e] = c.src[n * c.stride];
+    cv0[e] = o.contract_values[n * 3];
+    cv1[e] = o.contract_values[n * 3 + 1];
+    settle[e] = o.contract_high_settle[n];
+    target[e] = o.target_positions[n * P + player];
+  }
+#pragma unroll
+  for (int e = 0; e < kObsEnvsPerWave; ++e) {
+    const int64_t n = n0 + e;
+    if (n < N && lane < D)
+      o.values[n * D + j] = obs_value(c, j, perm[e], word[e], cv0[e], cv1[e], settle[e], target[e]);
+  }
+}
+
 inline unsigned grid_for(int64_t n) { return (unsigned)((n + kBlock - 1) / kBlock); }
 
 int launch_check(const GameMove &g, int64_t N, hipStream_t s) {
@@ -236,13 +343,25 @@ int astra_high_low_observation(const astra_hl_observation *o, void *stream) {
   for (const void *p : need)
     if (p == nullptr)
       return fail(ASTRA_ERR_INVALID_ARGUMENT, "astra_high_low_observation: null pointer");
+  const bool rows = 12 + 6 * (int64_t)o->players <= 64;  // one lane per column
 #ifdef ASTRA_HOST_EMULATION
   (void)stream;
-  for (int64_t i = 0; i < total; ++i) observation_element(*o, i);
+  if (rows) {
+    for (int64_t n = 0; n < o->num_envs; ++n)
+      for (int32_t j = 0; j < 12 + 6 * o->players; ++j) observation_column(*o, n, j);
+  } else {
+    for (int64_t i = 0; i < total; ++i) observation_element(*o, i);
+  }
   return ASTRA_OK;
 #else
-  hipLaunchKernelGGL(observation_kernel, dim3(grid_for(total)), dim3(kBlock), 0,
-                     as_stream(stream), *o, total);
+  if (rows) {
+    const int64_t waves = ((int64_t)o->num_envs + kObsEnvsPerWave - 1) / kObsEnvsPerWave;
+    hipLaunchKernelGGL(observation_rows_kernel, dim3(grid_for(waves * 64)), dim3(kBlock), 0,
+                       as_stream(stream), *o, (int64_t)o->num_envs);
+  } else {
+    hipLaunchKernelGGL(observation_kernel, dim3(grid_for(total)), dim3(kBlock), 0,
+                       as_stream(stream), *o, total);
+  }
   ASTRA_HIP_CHECK(rt_last_error(), "observation_kernel launch");
   return ASTRA_OK;
 #endif
