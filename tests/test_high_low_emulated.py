@@ -64,6 +64,8 @@ def _play(N, P, T, S, cM, V, shape, seed, obs_every=3, layout="columns", stage_b
     (64, 5, 6, 5, 5, 30, None, 2),
     (50, 5, 8, 3, 4, 20, (21, 12, 6, 5), 3),  # a ring of 12 wraps: slot reuse
     (40, 6, 4, 5, 5, 127, (128, 1024, 10, 16), 4),  # the config-5 shape (C > players)
+    (37, 7, 4, 5, 5, 30, None, 8),          # 7 and 10 (the most) players
+    (33, 10, 3, 5, 5, 30, None, 9),
 ])
 @pytest.mark.parametrize("layout", ["columns", "rows"])
 def test_emulated_game_vs_oracle(N, P, T, S, cM, V, shape, seed, layout):
