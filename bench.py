@@ -405,10 +405,7 @@ def bench_game(args):
     game_bytes = N * ((16 + 4 + 4 + 16 * P) + (16 + 4 + 28 + 24 * P))
     step_bytes = (24.0 * N * K + 32.0 * n_ins + 109.0 * n_fill + 8.0 * n_empty) / K + game_bytes
     achieved = step_bytes / (step_ms * 1e-3) / 1e9
-    traffic, traffic_src = (None, None)
-    if N == cfg.envs:
-        traffic, traffic_src = profile_traffic(f"game_move_config5_{cfg.name}_kernel_trace.md",
-                                               "quote_match_kernel<2, false, true, false, true>")
+    traffic, traffic_src = game_traffic(cfg, N)
     result = {
         "metric": "quote-matches/sec and market-steps/sec at 100k markets; p50 step latency",
         "value": N * K / wall,
@@ -598,6 +595,14 @@ def measured_traffic(cfg, M, bbo):
         words *= 2
     return profile_traffic(f"quote_match_config{cfg.index}_{cfg.name}_hbm_traffic.md",
                            f"quote_match_kernel<{words}, false, false, false, false>")
+
+
+def game_traffic(cfg, N):
+    """HBM bytes per fused game-move launch for this workload (see profile_traffic)."""
+    if N != cfg.envs:
+        return None, None
+    return profile_traffic(f"game_move_config5_{cfg.name}_kernel_trace.md",
+                           "quote_match_kernel<2, false, true, false, true>")
 
 
 def cpu_baseline(args, cfg, host, M, W, K, bbo):
