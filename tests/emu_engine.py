@@ -34,10 +34,11 @@ def build(force: bool = False) -> str:
         return EMU_LIB
     os.makedirs(BUILD_DIR, exist_ok=True)
     from astra_cuda.build import hipcc
+    tmp = f"{EMU_LIB}.{os.getpid()}.tmp"
     cmd = [hipcc(), "-DASTRA_HOST_EMULATION", "--cuda-host-only", "-O2", "-g", "-std=c++17",
-           "-fPIC", "-shared", f"-I{os.path.join(ROOT, 'include')}", *SRCS, "-o", EMU_LIB + ".tmp"]
+           "-fPIC", "-shared", f"-I{os.path.join(ROOT, 'include')}", *SRCS, "-o", tmp]
     subprocess.run(cmd, check=True, capture_output=True)
-    os.replace(EMU_LIB + ".tmp", EMU_LIB)
+    os.replace(tmp, EMU_LIB)  # atomic: parallel test workers each build their own copy
     return EMU_LIB
 
 
