@@ -138,7 +138,8 @@ class HighLowTradingState:
             self.inv_permutation = torch.zeros((N, P), **i32)
             self.target_positions = torch.zeros((N, P), **i32)
             self.player_last_positions = torch.zeros((N, P, 2), **i32)
-            self.player_contract_over_time = torch.zeros((N, P, T, 6), **i32)
+            # player_contract_over_time, stored env-minor (see the property below)
+            self._pcot = torch.zeros((T, P, 6, N), **i32)
             self.market_contract_over_time = torch.zeros((N, P * T, 3), **i32)
             self.immediate_rewards = torch.zeros((N, P), **i32)
             self.rewards_since_last_action = torch.zeros((N, P), **i32)
@@ -152,7 +153,7 @@ class HighLowTradingState:
             self.market = o.market.clone()
             for name in ("contract_values", "contract_high_settle", "player_permutation",
                          "inv_permutation", "target_positions", "player_last_positions",
-                         "player_contract_over_time", "market_contract_over_time",
+                         "_pcot", "market_contract_over_time",
                          "immediate_rewards", "rewards_since_last_action"):
                 setattr(self, name, getattr(o, name).clone())
             self.bbo_batch = o.bbo_batch.clone()
@@ -164,6 +165,14 @@ class HighLowTradingState:
         self._lib = _native.lib()
         self._trade = self._make_trade_args()
 
+    @property
+    def player_contract_over_time(self) -> torch.Tensor:
+        """The reference's [N,P,T,6] tensor (bid_px, ask_px, bid_sz, ask_sz, contracts,
+        cash per player and round, high_low_trading.h:109) as a view. The storage is
+        [T,P,6,N], env-minor, so that the move's stores and the observation's loads of
+        consecutive envs touch adjacent words."""
+        return self._pcot.permute(3, 1, 0, 2)
+
     def _make_trade_args(self):
         g = self._game
         t = _native.HLTrade()
@@ -171,7 +180,7 @@ class HighLowTradingState:
         ptrs = {
             "player_last_positions": self.player_last_positions,
             "target_positions": self.target_positions, "contract_values": self.contract_values,
-            "player_contract_over_time": self.player_contract_over_time,
+            "player_contract_over_time": self._pcot,
             "market_contract_over_time": self.market_contract_over_time,
             "immediate_rewards": self.immediate_rewards,
             "rewards_since_last_action": self.rewards_since_last_action,
@@ -263,7 +272,7 @@ class HighLowTradingState:
         self._move_number = 0
         for t in (self.contract_values, self.contract_high_settle, self.player_permutation,
                   self.inv_permutation, self.target_positions, self.player_last_positions,
-                  self.player_contract_over_time, self.market_contract_over_time,
+                  self._pcot, self.market_contract_over_time,
                   self.immediate_rewards, self.rewards_since_last_action):
             t.zero_()
         self.market.reset()
@@ -392,7 +401,7 @@ class HighLowTradingState:
         o.contract_values = self.contract_values.data_ptr()
         o.contract_high_settle = self.contract_high_settle.data_ptr()
         o.target_positions = self.target_positions.data_ptr()
-        o.player_contract_over_time = self.player_contract_over_time.data_ptr()
+        o.player_contract_over_time = self._pcot.data_ptr()
         bb = self.bbo_batch
         o.best_bid_prices = bb.best_bid_prices.data_ptr()
         o.best_ask_prices = bb.best_ask_prices.data_ptr()
@@ -413,7 +422,7 @@ class HighLowTradingState:
     def expose_info(self) -> dict:  # :475-485
         if not self.is_terminal():
             _fatal("ExposeInfo called on non-terminal state")
-        return {"players": self.player_contract_over_time.clone(),
+        return {"players": self.player_contract_over_time.clone(memory_format=torch.contiguous_format),
                 "market": self.market_contract_over_time.clone(),
                 "target_positions": self.target_positions.clone()}
 

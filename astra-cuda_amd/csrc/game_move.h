@@ -20,7 +20,8 @@ struct GameMove {
   int32_t *last_pos;            // [M,P,2]
   const int32_t *target;        // [M,P]
   const int32_t *contract_values;  // [M,3]
-  int32_t *pcot;                // [M,P,T,6]
+  int32_t *pcot;                // [T,P,6,M]: env-minor, word (m,p,t,f) at ((t*P+p)*6+f)*M+m
+                                // (M = the market's env count)
   int32_t *mcot;                // [M,P*T,3]
   int32_t *imm, *rsla;          // [M,P]
   int32_t *bbo_out[4];          // best bid px, bid size, ask px, ask size [M]
@@ -126,10 +127,10 @@ ASTRA_HD void game_before(const GameMove &g, const GameSnap &snap, const int32_t
 }
 
 // After the matching (its fill rows and portfolio atomics issued): BBO, last
-// price, telemetry and rewards of env m. fills = this call's fill count,
+// price, telemetry and rewards of env m of M. fills = this call's fill count,
 // last_px = the price of its last fill row.
-ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *pf_m, int64_t m,
-                         const int32_t (&bbo)[4], int32_t fills, int32_t last_px) {
+ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *pf_m, int64_t M,
+                         int64_t m, const int32_t (&bbo)[4], int32_t fills, int32_t last_px) {
   for (int k = 0; k < 4; ++k) g.bbo_out[k][m] = bbo[k];
   int32_t last = g.last_prices[m];
   if (fills > 0) {  // UpdateLastPrices (market.cu:767-786)
@@ -137,12 +138,14 @@ ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *p
     g.last_prices[m] = last;
   }
   const int32_t P = g.P, T = g.T, V = g.V, player = g.player, tmn = g.tmn, pmn = tmn / P;
-  int32_t *pc = g.pcot + m * P * (int64_t)T * 6;
-  int32_t *mine = pc + ((int64_t)player * T + pmn) * 6;
+  // this round's rows of env m: word (p, f) at (p*6+f)*M, so a wavefront's lanes
+  // store consecutive words
+  int32_t *pc = g.pcot + (int64_t)pmn * P * 6 * M + m;
+  int32_t *mine = pc + (int64_t)player * 6 * M;
   mine[0] = q.bid_px;
-  mine[1] = q.ask_px;
-  mine[2] = q.bid_sz;
-  mine[3] = q.ask_sz;
+  mine[M] = q.ask_px;
+  mine[2 * M] = q.bid_sz;
+  mine[3 * M] = q.ask_sz;
   int32_t *mc = g.mcot + (m * (int64_t)P * T + tmn) * 3;
   mc[0] = bbo[0];
   mc[1] = bbo[2];
@@ -174,8 +177,8 @@ ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *p
     for (int32_t j = 0; j < kPlayerBatch; ++j) {
       const int32_t p = p0 + j;
       if (p < P) {
-        pc[((int64_t)p * T + pmn) * 6 + 4] = c_con[j];
-        pc[((int64_t)p * T + pmn) * 6 + 5] = c_cash[j];
+        pc[((int64_t)p * 6 + 4) * M] = c_con[j];
+        pc[((int64_t)p * 6 + 5) * M] = c_cash[j];
         int32_t r = tgt[j] != 0
                         ? g_mul(g_sub(g_abs(g_sub(l_con[j], tgt[j])), g_abs(g_sub(c_con[j], tgt[j]))), V)
                         : 0;

@@ -49,7 +49,7 @@ ASTRA_HD void trade_check(const GameMove &g, int64_t n) {
 
 // One element of the [N, 6 + 1 + 6P + 5] observation (:510-602).
 ASTRA_HD void observation_element(const astra_hl_observation &o, int64_t i) {
-  const int32_t P = o.players, T = o.steps_per_player, player = o.player, cr = o.current_round;
+  const int32_t P = o.players, player = o.player, cr = o.current_round;
   const int64_t D = 6 + 1 + 6 * (int64_t)P + 5;
   const int64_t n = i / D;
   const int32_t j = (int32_t)(i - n * D);
@@ -78,7 +78,7 @@ ASTRA_HD void observation_element(const astra_hl_observation &o, int64_t i) {
     if (cr == 0 || player == P - 1) r = cr;
     else if (player == 0) r = cr - 1;
     else r = p < player ? cr : cr - 1;
-    v = (float)o.player_contract_over_time[((n * P + p) * T + r) * 6 + f];
+    v = (float)o.player_contract_over_time[(((int64_t)r * P + p) * 6 + f) * o.num_envs + n];
   } else {  // BBO and last price (:589-599)
     const int32_t k = j - (7 + 6 * P);
     const int32_t *src = k == 0   ? o.best_bid_prices
@@ -122,7 +122,7 @@ struct ObsColumn {
 };
 
 ASTRA_HD ObsColumn obs_column(const astra_hl_observation &o, int32_t j) {
-  const int32_t P = o.players, T = o.steps_per_player, player = o.player, cr = o.current_round;
+  const int32_t P = o.players, player = o.player, cr = o.current_round;
   ObsColumn c{o.player_permutation + player, P, 0, 0.0f};
   if (j <= 2) {
     c.kind = 0;
@@ -137,8 +137,8 @@ ASTRA_HD ObsColumn obs_column(const astra_hl_observation &o, int32_t j) {
     if (cr == 0 || player == P - 1) r = cr;
     else if (player == 0) r = cr - 1;
     else r = p < player ? cr : cr - 1;
-    c.src = o.player_contract_over_time + ((int64_t)p * T + r) * 6 + f;
-    c.stride = (int64_t)P * T * 6;
+    c.src = o.player_contract_over_time + (((int64_t)r * P + p) * 6 + f) * o.num_envs;
+    c.stride = 1;
     c.kind = 3;
   } else {  // BBO and last price (:589-599)
     const int32_t k = j - (7 + 6 * P);

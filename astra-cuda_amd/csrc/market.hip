@@ -1085,7 +1085,7 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
   }
   if (GAME) {
     const int32_t bbo[4] = {obp, obs, oap, oas};
-    game_after(game, c.gq, c.pf, m, bbo, s.fc, s.last_px);
+    game_after(game, c.gq, c.pf, M, m, bbo, s.fc, s.last_px);
   }
   if (MULTI) {
     if (so.counts) so.counts[m] = s.fc;

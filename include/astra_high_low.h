@@ -45,7 +45,9 @@ typedef struct astra_hl_trade {
   int32_t *player_last_positions; /* [N,P,2] */
   const int32_t *target_positions;/* [N,P] */
   const int32_t *contract_values; /* [N,3] */
-  int32_t *player_contract_over_time; /* [N,P,T,6] */
+  int32_t *player_contract_over_time; /* the reference's [N,P,T,6] tensor stored env-minor,
+                                         as [T,P,6,N]: word (n,p,t,f) at ((t*P+p)*6+f)*N+n,
+                                         so that consecutive envs' words are adjacent */
   int32_t *market_contract_over_time; /* [N,P*T,3] */
   int32_t *immediate_rewards;     /* [N,P] */
   int32_t *rewards_since_last_action; /* [N,P] */
@@ -82,7 +84,7 @@ typedef struct astra_hl_observation {
   const int32_t *contract_values; /* [N,3] */
   const uint8_t *contract_high_settle; /* [N] */
   const int32_t *target_positions;/* [N,P] */
-  const int32_t *player_contract_over_time; /* [N,P,T,6] */
+  const int32_t *player_contract_over_time; /* [T,P,6,N], as astra_hl_trade keeps it */
   const int32_t *best_bid_prices, *best_ask_prices, *best_bid_sizes, *best_ask_sizes, *last_prices;
   int32_t num_envs, players, steps_per_player, player, current_round;
   float player_sin, player_cos;   /* sin, cos of 2*pi*player/P, computed in double (:532-534) */

@@ -268,7 +268,7 @@ class EmuHighLow:
         self.player_permutation = z(N, P)
         self.target_positions = z(N, P)
         self.player_last_positions = z(N, P, 2)
-        self.player_contract_over_time = z(N, P, T, 6)
+        self._pcot = z(T, P, 6, N)  # env-minor, as the C ABI keeps it
         self.market_contract_over_time = z(N, P * T, 3)
         self.immediate_rewards = z(N, P)
         self.rewards_since_last_action = z(N, P)
@@ -276,15 +276,21 @@ class EmuHighLow:
         self.errors_host = z(1)
         self._HLTrade, self._HLObservation = HLTrade, HLObservation
 
+    @property
+    def player_contract_over_time(self):
+        """[N,P,T,6] view of the env-minor [T,P,6,N] storage."""
+        return np.transpose(self._pcot, (3, 1, 0, 2))
+
     def trade(self, move, player, tmn, check=1):
         self.move = np.ascontiguousarray(move, np.int32)
         t = self._HLTrade()
         ptr = lambda a: a.ctypes.data  # noqa: E731
         for name in ("player_last_positions", "target_positions", "contract_values",
-                     "player_contract_over_time", "market_contract_over_time", "immediate_rewards",
+                     "market_contract_over_time", "immediate_rewards",
                      "rewards_since_last_action", "errors", "errors_host"):
             a = getattr(self, name)
             setattr(t, name, None if a is None else ptr(a))
+        t.player_contract_over_time = ptr(self._pcot)
         t.move = ptr(self.move)
         if isinstance(self.fills, EmuRowFills):
             t.fill_rows, t.fill_counts = ptr(self.fills.rows), ptr(self.fills.fill_counts)
@@ -308,7 +314,7 @@ class EmuHighLow:
         o.contract_values = ptr(self.contract_values)
         o.contract_high_settle = ptr(self.contract_high_settle)
         o.target_positions = ptr(self.target_positions)
-        o.player_contract_over_time = ptr(self.player_contract_over_time)
+        o.player_contract_over_time = ptr(self._pcot)
         o.best_bid_prices, o.best_ask_prices = ptr(self.bbo.best_bid_prices), ptr(self.bbo.best_ask_prices)
         o.best_bid_sizes, o.best_ask_sizes = ptr(self.bbo.best_bid_sizes), ptr(self.bbo.best_ask_sizes)
         o.last_prices = ptr(self.bbo.last_prices)

@@ -97,6 +97,8 @@ def test_gpu_game_vs_oracle(N, P, T, S, cM, V, shape, seed, budget):
     assert np.array_equal(o.fill_returns(), ret.cpu().numpy())
     info = s.expose_info()
     assert np.array_equal(info["players"].cpu().numpy(), o.player_contract_over_time)
+    # a copy in the reference's layout, not a view of the env-minor storage
+    assert info["players"].is_contiguous() and info["players"].shape == (o.N, o.P, o.T, 6)
     assert np.array_equal(info["market"].cpu().numpy(), o.market_contract_over_time)
     for mv in moves[clone_at + 1:]:
         s2.apply_action(_t(mv))
