@@ -101,15 +101,6 @@ __global__ __launch_bounds__(kBlock) void observation_kernel(astra_hl_observatio
   if (i < total) observation_element(o, i);
 }
 
-// The same observation with one lane per column and a wavefront per
-// kObsEnvsPerWave envs, for rows of at most 64 columns (P <= 8). A column's
-// source is fixed for the call, so every lane loads its column's word of all its
-// envs, and the env's shared words (permutation entry, contract values, settle
-// flag, target) as loads every lane makes alike, before anything waits; the
-// per-element kernel above branches on the column and waits once per branch.
-// Consecutive lanes write consecutive columns of a row.
-constexpr int kObsEnvsPerWave = 16;
-
 // Column j's source (:510-602): kind 0 = one-hot of the permutation entry
 // (j 0-2), 1 = a constant (j 3, 4, 6), 2 = the private information (j 5),
 // 3 = src[n * stride] (the rounds of player_contract_over_time, then the BBO and
@@ -180,32 +171,42 @@ ASTRA_HD void observation_column(const astra_hl_observation &o, int64_t n, int32
                 o.contract_high_settle[n], o.target_positions[n * P + o.player]);
 }
 
-__global__ __launch_bounds__(kBlock) void observation_rows_kernel(astra_hl_observation o,
-                                                                  int64_t N) {
-  const int lane = (int)(threadIdx.x % 64);
-  const int64_t n0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64 * kObsEnvsPerWave;
+// The same observation with one lane per env, for rows of at most 64 columns
+// (P <= 8). A column's source is fixed for the call, and consecutive envs' words
+// are adjacent in every source (the env-minor player_contract_over_time, the [N]
+// BBO arrays), so a wavefront loads each column of its 64 envs with one
+// coalesced load, all columns before any wait (the per-element kernel above
+// branches on the column and waits once per branch); it transposes the values in
+// LDS and stores its 64 rows, which are contiguous in `values`, a row per store.
+constexpr int kObsTileWaves = 2;     // wavefronts per block
+constexpr int kObsMaxColumns = 64;
+
+__global__ __launch_bounds__(kObsTileWaves * 64) void observation_tile_kernel(astra_hl_observation o,
+                                                                             int64_t N) {
+  extern __shared__ float obs_tile[];  // per wavefront: 64 rows of `pitch` floats
+  const int lane = (int)(threadIdx.x % 64), w = (int)(threadIdx.x / 64);
+  const int64_t n0 = ((int64_t)blockIdx.x * kObsTileWaves + w) * 64;
   const int32_t P = o.players, player = o.player, D = 12 + 6 * P;
-  const int32_t j = lane < D ? lane : D - 1;  // lanes past the row repeat its last column
-  const ObsColumn c = obs_column(o, j);
-  int32_t perm[kObsEnvsPerWave], word[kObsEnvsPerWave], cv0[kObsEnvsPerWave];
-  int32_t cv1[kObsEnvsPerWave], target[kObsEnvsPerWave];
-  uint8_t settle[kObsEnvsPerWave];
+  const int32_t pitch = D + 1;  // odd (D is even): lanes' rows fall in different banks
+  const int64_t n = n0 + lane < N ? n0 + lane : N - 1;  // clamped: no branch around a load
+  const int32_t perm = o.player_permutation[n * P + player];
+  const int32_t cv0 = o.contract_values[n * 3], cv1 = o.contract_values[n * 3 + 1];
+  const uint8_t settle = o.contract_high_settle[n];
+  const int32_t target = o.target_positions[n * P + player];
+  int32_t word[kObsMaxColumns];
 #pragma unroll
-  for (int e = 0; e < kObsEnvsPerWave; ++e) {  // env index clamped: no branch around a load
-    const int64_t n = n0 + e < N ? n0 + e : N - 1;
-    perm[e] = o.player_permutation[n * P + player];
-    word[e] = c.src[n * c.stride];
-    cv0[e] = o.contract_values[n * 3];
-    cv1[e] = o.contract_values[n * 3 + 1];
-    settle[e] = o.contract_high_settle[n];
-    target[e] = o.target_positions[n * P + player];
+  for (int32_t j = 0; j < kObsMaxColumns; ++j) {  // columns past the row reload the last one
+    const ObsColumn c = obs_column(o, j < D ? j : D - 1);
+    word[j] = c.src[n * c.stride];
   }
+  float *tile = obs_tile + w * 64 * pitch;
 #pragma unroll
-  for (int e = 0; e < kObsEnvsPerWave; ++e) {
-    const int64_t n = n0 + e;
-    if (n < N && lane < D)
-      o.values[n * D + j] = obs_value(c, j, perm[e], word[e], cv0[e], cv1[e], settle[e], target[e]);
-  }
+  for (int32_t j = 0; j < kObsMaxColumns; ++j)
+    if (j < D)
+      tile[lane * pitch + j] = obs_value(obs_column(o, j), j, perm, word[j], cv0, cv1, settle, target);
+  __syncthreads();
+  if (lane < D)
+    for (int32_t e = 0; e < 64 && n0 + e < N; ++e) o.values[(n0 + e) * D + lane] = tile[e * pitch + lane];
 }
 
 inline unsigned grid_for(int64_t n) { return (unsigned)((n + kBlock - 1) / kBlock); }
@@ -355,8 +356,10 @@ int astra_high_low_observation(const astra_hl_observation *o, void *stream) {
   return ASTRA_OK;
 #else
   if (rows) {
-    const int64_t waves = ((int64_t)o->num_envs + kObsEnvsPerWave - 1) / kObsEnvsPerWave;
-    hipLaunchKernelGGL(observation_rows_kernel, dim3(grid_for(waves * 64)), dim3(kBlock), 0,
+    const int64_t per_block = 64 * kObsTileWaves;
+    const unsigned blocks = (unsigned)(((int64_t)o->num_envs + per_block - 1) / per_block);
+    const size_t lds = (size_t)per_block * (13 + 6 * o->players) * sizeof(float);
+    hipLaunchKernelGGL(observation_tile_kernel, dim3(blocks), dim3(per_block), lds,
                        as_stream(stream), *o, (int64_t)o->num_envs);
   } else {
     hipLaunchKernelGGL(observation_kernel, dim3(grid_for(total)), dim3(kBlock), 0,

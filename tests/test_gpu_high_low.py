@@ -65,8 +65,8 @@ def _params(N, P, T, S, cM, V, shape):
     (300, 8, 3, 5, 5, 30, None, 4, 1),     # 8 and 9 players, staging forced
     (300, 9, 3, 5, 5, 30, None, 5, 1),
     (300, 5, 8, 3, 4, 20, (21, 12, 6, 5), 6, 1),
-    (37, 7, 4, 5, 5, 30, None, 7, None),   # 7 and 10 (the most) players; env counts that are not
-    (33, 10, 3, 5, 5, 30, None, 8, None),  # multiples of the observation's 16 envs per wave
+    (37, 7, 4, 5, 5, 30, None, 7, None),   # 7 players: the observation's tile of 64 envs, ragged
+    (33, 10, 3, 5, 5, 30, None, 8, None),  # 10 (the most): the per-element observation kernel
 ])
 def test_gpu_game_vs_oracle(N, P, T, S, cM, V, shape, seed, budget):
     print(f"game N={N} P={P} T={T} shape={shape} stage budget {budget}", flush=True)
