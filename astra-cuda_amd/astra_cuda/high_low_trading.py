@@ -140,7 +140,8 @@ class HighLowTradingState:
             self.player_last_positions = torch.zeros((N, P, 2), **i32)
             # player_contract_over_time, stored env-minor (see the property below)
             self._pcot = torch.zeros((T, P, 6, N), **i32)
-            self.market_contract_over_time = torch.zeros((N, P * T, 3), **i32)
+            # market_contract_over_time, stored env-minor (see the property below)
+            self._mcot = torch.zeros((P * T, 3, N), **i32)
             self.immediate_rewards = torch.zeros((N, P), **i32)
             self.rewards_since_last_action = torch.zeros((N, P), **i32)
             self.bbo_batch = self.market.new_bbo_batch()
@@ -153,7 +154,7 @@ class HighLowTradingState:
             self.market = o.market.clone()
             for name in ("contract_values", "contract_high_settle", "player_permutation",
                          "inv_permutation", "target_positions", "player_last_positions",
-                         "_pcot", "market_contract_over_time",
+                         "_pcot", "_mcot",
                          "immediate_rewards", "rewards_since_last_action"):
                 setattr(self, name, getattr(o, name).clone())
             self.bbo_batch = o.bbo_batch.clone()
@@ -173,6 +174,13 @@ class HighLowTradingState:
         consecutive envs touch adjacent words."""
         return self._pcot.permute(3, 1, 0, 2)
 
+    @property
+    def market_contract_over_time(self) -> torch.Tensor:
+        """The reference's [N,P*T,3] tensor (best bid, best ask, last price after each
+        trading move, high_low_trading.h:110) as a view of [P*T,3,N] storage, env-minor
+        like player_contract_over_time."""
+        return self._mcot.permute(2, 0, 1)
+
     def _make_trade_args(self):
         g = self._game
         t = _native.HLTrade()
@@ -181,7 +189,7 @@ class HighLowTradingState:
             "player_last_positions": self.player_last_positions,
             "target_positions": self.target_positions, "contract_values": self.contract_values,
             "player_contract_over_time": self._pcot,
-            "market_contract_over_time": self.market_contract_over_time,
+            "market_contract_over_time": self._mcot,
             "immediate_rewards": self.immediate_rewards,
             "rewards_since_last_action": self.rewards_since_last_action,
             "errors": self._errors,
@@ -272,7 +280,7 @@ class HighLowTradingState:
         self._move_number = 0
         for t in (self.contract_values, self.contract_high_settle, self.player_permutation,
                   self.inv_permutation, self.target_positions, self.player_last_positions,
-                  self._pcot, self.market_contract_over_time,
+                  self._pcot, self._mcot,
                   self.immediate_rewards, self.rewards_since_last_action):
             t.zero_()
         self.market.reset()
@@ -422,8 +430,9 @@ class HighLowTradingState:
     def expose_info(self) -> dict:  # :475-485
         if not self.is_terminal():
             _fatal("ExposeInfo called on non-terminal state")
-        return {"players": self.player_contract_over_time.clone(memory_format=torch.contiguous_format),
-                "market": self.market_contract_over_time.clone(),
+        cf = torch.contiguous_format  # copies in the reference's layout, not views of the storage
+        return {"players": self.player_contract_over_time.clone(memory_format=cf),
+                "market": self.market_contract_over_time.clone(memory_format=cf),
                 "target_positions": self.target_positions.clone()}
 
     # ---- text renderings (:398-466, :603-804); copies the tensors to the host ----

@@ -22,7 +22,7 @@ struct GameMove {
   const int32_t *contract_values;  // [M,3]
   int32_t *pcot;                // [T,P,6,M]: env-minor, word (m,p,t,f) at ((t*P+p)*6+f)*M+m
                                 // (M = the market's env count)
-  int32_t *mcot;                // [M,P*T,3]
+  int32_t *mcot;                // [P*T,3,M]: env-minor, word (m,k,f) at (k*3+f)*M+m
   int32_t *imm, *rsla;          // [M,P]
   int32_t *bbo_out[4];          // best bid px, bid size, ask px, ask size [M]
   int32_t *last_prices;         // [M]
@@ -146,10 +146,10 @@ ASTRA_HD void game_after(const GameMove &g, const GameQuote &q, const int32_t *p
   mine[M] = q.ask_px;
   mine[2 * M] = q.bid_sz;
   mine[3 * M] = q.ask_sz;
-  int32_t *mc = g.mcot + (m * (int64_t)P * T + tmn) * 3;
+  int32_t *mc = g.mcot + (int64_t)tmn * 3 * M + m;
   mc[0] = bbo[0];
-  mc[1] = bbo[2];
-  mc[2] = last;
+  mc[M] = bbo[2];
+  mc[2 * M] = last;
   const int32_t mn = q.bid_sz < q.ask_sz ? q.bid_sz : q.ask_sz;
   const int32_t cross = g_add(g_sub(q.bid_px, q.ask_px), 1);
   const int32_t penalty = g_mul(g_mul(g_add(mn, 1), cross > 0 ? cross : 0), V);  // :308

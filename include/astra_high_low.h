@@ -48,7 +48,8 @@ typedef struct astra_hl_trade {
   int32_t *player_contract_over_time; /* the reference's [N,P,T,6] tensor stored env-minor,
                                          as [T,P,6,N]: word (n,p,t,f) at ((t*P+p)*6+f)*N+n,
                                          so that consecutive envs' words are adjacent */
-  int32_t *market_contract_over_time; /* [N,P*T,3] */
+  int32_t *market_contract_over_time; /* the reference's [N,P*T,3] stored env-minor, as
+                                         [P*T,3,N]: word (n,k,f) at (k*3+f)*N+n */
   int32_t *immediate_rewards;     /* [N,P] */
   int32_t *rewards_since_last_action; /* [N,P] */
   /* FillBatch (market.h:64-92) and BBOBatch (market.h:95-119) of the env's market */

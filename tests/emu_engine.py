@@ -269,7 +269,7 @@ class EmuHighLow:
         self.target_positions = z(N, P)
         self.player_last_positions = z(N, P, 2)
         self._pcot = z(T, P, 6, N)  # env-minor, as the C ABI keeps it
-        self.market_contract_over_time = z(N, P * T, 3)
+        self._mcot = z(P * T, 3, N)  # env-minor, as the C ABI keeps it
         self.immediate_rewards = z(N, P)
         self.rewards_since_last_action = z(N, P)
         self.errors = z(1)
@@ -281,16 +281,21 @@ class EmuHighLow:
         """[N,P,T,6] view of the env-minor [T,P,6,N] storage."""
         return np.transpose(self._pcot, (3, 1, 0, 2))
 
+    @property
+    def market_contract_over_time(self):
+        """[N,P*T,3] view of the env-minor [P*T,3,N] storage."""
+        return np.transpose(self._mcot, (2, 0, 1))
+
     def trade(self, move, player, tmn, check=1):
         self.move = np.ascontiguousarray(move, np.int32)
         t = self._HLTrade()
         ptr = lambda a: a.ctypes.data  # noqa: E731
         for name in ("player_last_positions", "target_positions", "contract_values",
-                     "market_contract_over_time", "immediate_rewards",
-                     "rewards_since_last_action", "errors", "errors_host"):
+                     "immediate_rewards", "rewards_since_last_action", "errors", "errors_host"):
             a = getattr(self, name)
             setattr(t, name, None if a is None else ptr(a))
         t.player_contract_over_time = ptr(self._pcot)
+        t.market_contract_over_time = ptr(self._mcot)
         t.move = ptr(self.move)
         if isinstance(self.fills, EmuRowFills):
             t.fill_rows, t.fill_counts = ptr(self.fills.rows), ptr(self.fills.fill_counts)

@@ -100,6 +100,7 @@ def test_gpu_game_vs_oracle(N, P, T, S, cM, V, shape, seed, budget):
     # a copy in the reference's layout, not a view of the env-minor storage
     assert info["players"].is_contiguous() and info["players"].shape == (o.N, o.P, o.T, 6)
     assert np.array_equal(info["market"].cpu().numpy(), o.market_contract_over_time)
+    assert info["market"].is_contiguous() and info["market"].shape == (o.N, o.P * o.T, 3)
     for mv in moves[clone_at + 1:]:
         s2.apply_action(_t(mv))
     _compare(o, s2, "clone")
