@@ -13,8 +13,10 @@ work fused, plus a check launch and one host wait, for the checks only, while
 the move kernel runs (the reference makes eight syncs); a move that fails a
 check changes nothing and raises. ``check_moves=False`` drops the check and the
 wait, and
-``check_errors()`` then reports any move that failed a check. The chance moves
-(:136-226), rewards, returns and reset are the reference's tensor operations.
+``check_errors()`` then reports any move that failed a check. FillRewards and
+FillRewardsSinceLastAction (:331-343) convert into a float32 buffer on a HIP
+kernel too. The chance moves (:136-226), returns and reset are the reference's
+tensor operations.
 """
 from __future__ import annotations
 
@@ -365,12 +367,24 @@ class HighLowTradingState:
     def fill_rewards(self, reward_buffer: torch.Tensor) -> None:
         _assert(reward_buffer.dim() == 2 and reward_buffer.size(0) == self._N and reward_buffer.size(1) == self._P,
                 "reward_buffer shape == [num_envs, num_players]")
-        reward_buffer.copy_(self.immediate_rewards)
+        self._rewards_to(reward_buffer, self.immediate_rewards, -1)
 
     def fill_rewards_since_last_action(self, reward_buffer: torch.Tensor, player_id: int) -> None:
         _assert(reward_buffer.dim() == 1 and reward_buffer.size(0) == self._N,
                 "reward_buffer shape == [num_envs]")
-        reward_buffer.copy_(self.rewards_since_last_action[:, player_id])
+        if 0 <= player_id < self._P:
+            self._rewards_to(reward_buffer, self.rewards_since_last_action, player_id)
+        else:  # the reference's index error
+            reward_buffer.copy_(self.rewards_since_last_action[:, player_id])
+
+    def _rewards_to(self, buf: torch.Tensor, src: torch.Tensor, player: int) -> None:
+        """buf.copy_(src, or its column `player`) on the HIP kernel for a contiguous
+        float32 buffer on the game's device; torch's copy_ for any other buffer."""
+        if buf.dtype == torch.float32 and buf.is_contiguous() and buf.device == self._dev:
+            _check(self._lib.astra_high_low_rewards(src.data_ptr(), self._N, self._P, player,
+                                                    buf.data_ptr(), _raw_stream(self._game.device_id)))
+        else:
+            buf.copy_(src if player < 0 else src[:, player])
 
     def fill_returns(self, returns_buffer: torch.Tensor) -> None:
         _assert(returns_buffer.dim() == 2 and returns_buffer.size(0) == self._N and returns_buffer.size(1) == self._P,

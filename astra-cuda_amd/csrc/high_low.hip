@@ -209,6 +209,27 @@ __global__ __launch_bounds__(kObsTileWaves * 64) void observation_tile_kernel(as
     for (int32_t e = 0; e < 64 && n0 + e < N; ++e) o.values[(n0 + e) * D + lane] = tile[e * pitch + lane];
 }
 
+// The rewards as float32: column `col` of the [n, stride] int32 array (col >= 0),
+// or all n words, four per lane with 16-byte accesses when `vec` (both pointers
+// 16-byte aligned). A plain int32 -> float32 conversion, as libtorch's copy_.
+__global__ __launch_bounds__(kBlock) void rewards_kernel(const int32_t *src, float *dst, int64_t n,
+                                                         int32_t stride, int32_t col, int32_t vec) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= 0) {
+    if (i < n) dst[i] = (float)src[i * stride + col];
+  } else if (vec) {
+    const int64_t k = i * 4;
+    if (k + 4 <= n) {
+      const int4 v = *reinterpret_cast<const int4 *>(src + k);
+      *reinterpret_cast<float4 *>(dst + k) = make_float4((float)v.x, (float)v.y, (float)v.z, (float)v.w);
+    } else {
+      for (int64_t q = k; q < n; ++q) dst[q] = (float)src[q];
+    }
+  } else if (i < n) {
+    dst[i] = (float)src[i];
+  }
+}
+
 inline unsigned grid_for(int64_t n) { return (unsigned)((n + kBlock - 1) / kBlock); }
 
 int launch_check(const GameMove &g, int64_t N, hipStream_t s) {
@@ -325,6 +346,30 @@ int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *st
     return fail(ASTRA_ERR_INVALID_ARGUMENT, std::string("high_low_trading.cc ") + check_text(bits));
   }
   return ASTRA_OK;
+}
+
+int astra_high_low_rewards(const int32_t *src, int64_t num_envs, int32_t players, int32_t player,
+                           float *dst, void *stream) {
+  ASTRA_ABI_CHECK(num_envs, >=, 0);
+  ASTRA_ABI_CHECK(players, >=, 1);
+  ASTRA_ABI_CHECK(player, <, players);
+  const int64_t n = player < 0 ? num_envs * players : num_envs;
+  if (n == 0) return ASTRA_OK;
+  if (src == nullptr || dst == nullptr)
+    return fail(ASTRA_ERR_INVALID_ARGUMENT, "astra_high_low_rewards: null pointer");
+  const int32_t col = player < 0 ? -1 : player;
+#ifdef ASTRA_HOST_EMULATION
+  (void)stream;
+  for (int64_t i = 0; i < n; ++i) dst[i] = (float)(col < 0 ? src[i] : src[i * players + col]);
+  return ASTRA_OK;
+#else
+  const int32_t vec = col < 0 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0);
+  const int64_t lanes = vec ? (n + 3) / 4 : n;
+  hipLaunchKernelGGL(rewards_kernel, dim3(grid_for(lanes)), dim3(kBlock), 0, as_stream(stream), src,
+                     dst, n, players, col, vec);
+  ASTRA_HIP_CHECK(rt_last_error(), "rewards_kernel launch");
+  return ASTRA_OK;
+#endif
 }
 
 int astra_high_low_observation(const astra_hl_observation *o, void *stream) {

@@ -94,6 +94,13 @@ typedef struct astra_hl_observation {
 
 int astra_high_low_observation(const astra_hl_observation *o, void *stream);
 
+/* FillRewards (high_low_trading.cc:331-336) with player < 0: dst[i] = (float)src[i] for
+ * all num_envs * players words; FillRewardsSinceLastAction (:338-343) with
+ * 0 <= player < players: dst[n] = (float)src[n * players + player]. src is the
+ * [N,P] int32 reward tensor, dst a contiguous float32 buffer. */
+int astra_high_low_rewards(const int32_t *src, int64_t num_envs, int32_t players, int32_t player,
+                           float *dst, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -221,3 +221,28 @@ def test_gpu_text_renderings():
                 assert s.to_string(idx) == oracle_to_string(o, idx), (k, idx)
                 for p in range(P):
                     assert s.observation_string(p, idx) == oracle_information_state_string(o, p, idx), (k, idx, p)
+
+
+@pytest.mark.parametrize("N,P", [(1, 4), (37, 7), (33, 10), (262144, 5)])
+def test_gpu_rewards_entry_point(N, P):
+    """astra_high_low_rewards against torch's int32 -> float32 copy_: the 16-byte path
+    (aligned buffers, word counts with a tail of 1-3), the one-word path (a buffer that
+    starts one float into its allocation) and one player's column."""
+    from astra_cuda import _native
+    print(f"rewards N={N} P={P}", flush=True)
+    lib = _native.lib()
+    g = torch.Generator().manual_seed(N + P)
+    src = torch.randint(-(1 << 30), 1 << 30, (N, P), dtype=torch.int32, generator=g).to(DEV)
+    want = src.float()
+    for off in (0, 1):
+        raw = torch.full((N * P + 4,), float("nan"), dtype=torch.float32, device=DEV)
+        dst = raw[off:off + N * P]
+        assert lib.astra_high_low_rewards(src.data_ptr(), N, P, -1, dst.data_ptr(), None) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(dst.view(N, P), want), off
+        assert torch.isnan(raw[off + N * P:]).all()  # nothing written past the end
+    for p in (0, P - 1):
+        col = torch.full((N,), float("nan"), dtype=torch.float32, device=DEV)
+        assert lib.astra_high_low_rewards(src.data_ptr(), N, P, p, col.data_ptr(), None) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(col, want[:, p]), p

@@ -134,3 +134,20 @@ def test_emulated_checks_flag_and_stop(host_word):
     e.errors[0] = 0
     assert e.trade(mv, 1, 1, check=0) == 0  # no check: trades, flag kept for the caller
     assert e.errors[0] == (1 << 0) | (1 << 6) and e.market.global_tid == tid + 2
+
+
+@pytest.mark.parametrize("N,P", [(1, 4), (37, 7), (33, 10), (0, 5)])
+def test_emulated_rewards_entry_point(N, P):
+    """astra_high_low_rewards (FillRewards / FillRewardsSinceLastAction,
+    high_low_trading.cc:331-343): int32 -> float32, all words or one player's column."""
+    from emu_engine import lib
+    rng = np.random.default_rng(N * 31 + P)
+    src = rng.integers(-(1 << 30), 1 << 30, size=(N, P), dtype=np.int32)
+    dst = np.full((N, P), np.nan, np.float32)
+    assert lib().astra_high_low_rewards(src.ctypes.data, N, P, -1, dst.ctypes.data, None) == 0
+    assert np.array_equal(dst, src.astype(np.float32))
+    for p in (0, P - 1):
+        col = np.full(N, np.nan, np.float32)
+        assert lib().astra_high_low_rewards(src.ctypes.data, N, P, p, col.ctypes.data, None) == 0
+        assert np.array_equal(col, src[:, p].astype(np.float32))
+    assert lib().astra_high_low_rewards(src.ctypes.data, N, P, P, dst.ctypes.data, None) != 0
