@@ -46,7 +46,11 @@ DEFAULT_PARAMETERS = {
 }
 # Not in the reference: override the market shape the game derives (:57-69), for
 # game-shaped benchmarks on larger books. num_customers must be >= players.
-MARKET_SHAPE_PARAMETERS = ("market_price_levels", "market_orders", "market_fills", "market_customers")
+# A shape beyond the reference's VecMarket caps (L <= 128, O <= 1024, F <= 1024,
+# C <= 1024) raises the reference's constructor error (market.cu:338-342) unless
+# market_extended_shapes is true.
+MARKET_SHAPE_PARAMETERS = ("market_price_levels", "market_orders", "market_fills", "market_customers",
+                           "market_extended_shapes")
 
 
 def _assert(cond: bool, what: str):
@@ -84,6 +88,7 @@ class HighLowTradingGame:
         )
         if self.market_shape[3] < self.players:
             _fatal("high_low_trading.py market_customers >= players")
+        self.market_extended_shapes = bool(p.get("market_extended_shapes", False))
 
     # core_bindings.cc:93-115
     def new_initial_state(self) -> "HighLowTradingState":
@@ -130,9 +135,8 @@ class HighLowTradingState:
         self._dev = torch.device("cuda", game.device_id)
         if _clone_of is None:
             L, O, F, C = game.market_shape
-            ext = L > 128 or O > 1024 or F > 1024 or C > 1024
             self.market = VecMarket(N, L, O, F, C, game.device_id, game.threads_per_block,
-                                    allow_extended_shapes=ext)
+                                    allow_extended_shapes=game.market_extended_shapes)
             i32 = dict(dtype=torch.int32, device=self._dev)
             self.contract_values = torch.zeros((N, 3), **i32)
             self.contract_high_settle = torch.zeros((N,), dtype=torch.bool, device=self._dev)
@@ -349,8 +353,14 @@ class HighLowTradingState:
             _fatal(_native.last_error())
 
     def set_check_moves(self, check: bool) -> None:
-        """Switch the per-move input checks (one host wait per move) on or off."""
+        """Switch the per-move input checks (one host wait per move) on or off.
+        Switching them on first reports (raises, like check_errors) any unchecked
+        move since the last check_errors() that failed a check, and clears the
+        error word, so the next checked move sees only its own checks."""
+        was = self._trade.check
         self._trade.check = 1 if check else 0
+        if check and not was:
+            self.check_errors()
 
     def check_errors(self) -> None:
         """With check_moves=False: raise if any move since the last call failed the

@@ -531,15 +531,16 @@ class VecMarket:
     # -- introspection (not in the reference binding) -------------------------
 
     def _set_stats(self, counters) -> None:
-        """Diagnostic: accumulate per-call work counts into an int64 [8] device tensor
+        """Diagnostic: accumulate per-call work counts into an int64 [10] device tensor
         (inserts, fill rows, emptied levels, overflowed markets, fast-forwarded
-        overflows); None switches it off."""
+        overflows, loop passes, staged markets, crossing markets, zero-size runs
+        listed on a staged book and their rows); None switches it off."""
         if counters is None:
             _check(self._lib.astra_market_set_stats(self._h, None))
             return
-        if (counters.dtype != torch.int64 or counters.numel() < 8 or counters.device != self._device
+        if (counters.dtype != torch.int64 or counters.numel() < 10 or counters.device != self._device
                 or not counters.is_contiguous()):
-            _fatal("stats counters must be a contiguous int64 tensor of >= 8 elements on the engine's device")
+            _fatal("stats counters must be a contiguous int64 tensor of >= 10 elements on the engine's device")
         self._stats_ref = counters
         _check(self._lib.astra_market_set_stats(self._h, counters.data_ptr()))
 

@@ -106,6 +106,7 @@ struct astra_market {
   int32_t tid;                // host TID counter, market.h:338
   int block;                  // launch block size of the per-market kernels
   int32_t stage_budget;       // loop passes before a market is staged in LDS (0: never)
+  int32_t lds_limit;          // LDS bytes a workgroup may use on the device
   int32_t per_wave;           // markets per wavefront of the matching kernel (0: default)
   unsigned long long *stats;  // see astra_market_set_stats
   char *ws;
@@ -123,7 +124,7 @@ struct Book {
   uint16_t *levels;           // [M][L][4] = {bid_head, bid_tail, ask_head, ask_tail}
   uint4 *records;             // [M][O] = {size, customer, tid, price | next << 16}
   int32_t *portfolios;        // [M][C][2] = {contracts, cash}
-  unsigned long long *stats;  // diagnostic counters [4] or nullptr
+  unsigned long long *stats;  // diagnostic counters [10] or nullptr
   int32_t M, L, O, F, C;
 };
 
@@ -293,10 +294,24 @@ struct Bulk {
   int32_t v[8];   // price, size, taker, quoter, is_sell_quote, quote_size, tid, quote_tid
 };
 
+// A store into the caller's fill batch through a global-address-space pointer.
+// The kernel holds the batch pointers in VGPRs (in_vgpr), where the compiler no
+// longer knows they point to global memory; plain stores through them become
+// flat stores, which also count against the LDS/scalar counter, so every later
+// wait for an LDS access would wait for those stores to reach memory too.
+template <class T>
+ASTRA_HD void gst(T *p, const T &v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  *(__attribute__((address_space(1))) T *)p = v;
+#else
+  *p = v;
+#endif
+}
+
 ASTRA_HD void write_row(int32_t *rows, int64_t fi, const int32_t (&v)[8]) {
   int4 *d = reinterpret_cast<int4 *>(rows + fi * 8);
-  d[0] = make_int4(v[0], v[1], v[2], v[3]);
-  d[1] = make_int4(v[4], v[5], v[6], v[7]);
+  gst(d, make_int4(v[0], v[1], v[2], v[3]));
+  gst(d + 1, make_int4(v[4], v[5], v[6], v[7]));
 }
 
 ASTRA_HD void write_fill(const FillOut &out, int64_t fi, const int32_t (&v)[8]) {
@@ -304,14 +319,14 @@ ASTRA_HD void write_fill(const FillOut &out, int64_t fi, const int32_t (&v)[8]) 
     write_row(out.rows, fi, v);
     return;
   }
-  out.prices[fi] = v[0];
-  out.sizes[fi] = v[1];
-  out.taker[fi] = v[2];
-  out.quoter[fi] = v[3];
-  out.is_sell_quote[fi] = (uint8_t)v[4];
-  out.quote_sizes[fi] = v[5];
-  out.tid[fi] = v[6];
-  out.quote_tid[fi] = v[7];
+  gst(out.prices + fi, v[0]);
+  gst(out.sizes + fi, v[1]);
+  gst(out.taker + fi, v[2]);
+  gst(out.quoter + fi, v[3]);
+  gst(out.is_sell_quote + fi, (uint8_t)v[4]);
+  gst(out.quote_sizes + fi, v[5]);
+  gst(out.tid + fi, v[6]);
+  gst(out.quote_tid + fi, v[7]);
 }
 
 // Host build: write the owed rows directly.
@@ -388,28 +403,29 @@ struct FillSink {
       const int f = fidx[j];
       if ((reinterpret_cast<uintptr_t>(d) & 15) == 0) {
         if (n == 4) {
-          *reinterpret_cast<int4 *>(d) = make_int4(at(f, 0), at(f, 1), at(f, 2), at(f, 3));
+          gst(reinterpret_cast<int4 *>(d), make_int4(at(f, 0), at(f, 1), at(f, 2), at(f, 3)));
         } else {
-          if (n & 2) *reinterpret_cast<int2 *>(d) = make_int2(at(f, 0), at(f, 1));
-          if (n & 1) d[n - 1] = at(f, n - 1);
+          if (n & 2) gst(reinterpret_cast<int2 *>(d), make_int2(at(f, 0), at(f, 1)));
+          if (n & 1) gst(d + (n - 1), at(f, n - 1));
         }
       } else {
-        for (int r = 0; r < n; ++r) d[r] = at(f, r);
+        for (int r = 0; r < n; ++r) gst(d + r, at(f, r));
       }
     }
     uint8_t *d8 = out.is_sell_quote + base;
     if ((reinterpret_cast<uintptr_t>(d8) & 3) == 0) {
       if (n == 4) {
-        *reinterpret_cast<uint32_t *>(d8) = (uint32_t)at(4, 0) | ((uint32_t)at(4, 1) << 8) |
-                                            ((uint32_t)at(4, 2) << 16) | ((uint32_t)at(4, 3) << 24);
+        gst(reinterpret_cast<uint32_t *>(d8),
+            (uint32_t)at(4, 0) | ((uint32_t)at(4, 1) << 8) | ((uint32_t)at(4, 2) << 16) |
+                ((uint32_t)at(4, 3) << 24));
       } else {
         if (n & 2)
-          *reinterpret_cast<uint16_t *>(d8) =
-              (uint16_t)((uint32_t)at(4, 0) | ((uint32_t)at(4, 1) << 8));
-        if (n & 1) d8[n - 1] = (uint8_t)at(4, n - 1);
+          gst(reinterpret_cast<uint16_t *>(d8),
+              (uint16_t)((uint32_t)at(4, 0) | ((uint32_t)at(4, 1) << 8)));
+        if (n & 1) gst(d8 + (n - 1), (uint8_t)at(4, n - 1));
       }
     } else {
-      for (int r = 0; r < n; ++r) d8[r] = (uint8_t)at(4, r);
+      for (int r = 0; r < n; ++r) gst(d8 + r, (uint8_t)at(4, r));
     }
     for (int r = 0; r < n; ++r)
       apply_portfolio(pf, C, at(0, r), at(1, r), at(2, r), at(3, r), at(4, r) != 0);
@@ -485,6 +501,7 @@ struct LoopState {
   int32_t last_px;             // price of the last fill row written
   uint32_t emptied, forwarded; // diagnostic counts
   uint32_t npass;
+  uint32_t zruns, zrows;       // zero-size walks on a staged book and their rows
 };
 
 // What one step of a multi-step launch hands its market's next step, in
@@ -609,6 +626,8 @@ ASTRA_HD LoopState<W> uniform_state(const LoopState<W> &a) {
   u.emptied = uni(a.emptied);
   u.forwarded = uni(a.forwarded);
   u.npass = uni(a.npass);
+  u.zruns = uni(a.zruns);
+  u.zrows = uni(a.zrows);
   return u;
 }
 
@@ -832,6 +851,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   s.fc = 0;
   s.last_px = 0;
   s.emptied = s.forwarded = s.npass = 0;
+  s.zruns = s.zrows = 0;
 }
 
 // The fill row of one pass (market.cu:172-218): the earlier TID rests (ties go
@@ -855,7 +875,7 @@ ASTRA_HD void make_row(const uint4 &b, const uint4 &a, int32_t qty, int32_t (&ro
 // the level's head once at the end. Called at the top of a pass with both
 // records loaded; returns false when the budget or the sink stopped it (state
 // intact at the top of a pass).
-template <int SIDE, int W, class BookMem, class Sink>
+template <int SIDE, bool STATS, int W, class BookMem, class Sink>
 ASTRA_HD bool zero_walk(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, Sink &sink,
                         const FillOut &out, int32_t budget, int32_t &passes) {
   uint4 &w = SIDE == 0 ? s.brec : s.arec;
@@ -864,12 +884,13 @@ ASTRA_HD bool zero_walk(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, 
   bool ok = true;
   for (;;) {
     const uint32_t nh = rec_next(w);
-    if (nh == kNull16 || nh == h || s.fc >= c.F) break;
+    if (nh >= (uint32_t)c.O || nh == h || s.fc >= c.F) break;  // NULL (or out of range) ends it
     int32_t row[8];
     make_row(s.brec, s.arec, 0, row);
     sink.put(out, c.pf, c.C, row);
     s.last_px = row[0];
     ++s.fc;
+    if (STATS) ++s.zrows;
     h = nh;
     w = bk.record(nh);
     if (passes++ >= budget || sink.full()) {
@@ -878,7 +899,10 @@ ASTRA_HD bool zero_walk(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, 
     }
     if ((int32_t)w.x != 0 || s.bh == s.ah) break;
   }
-  if (h != start) bk.set_head(SIDE == 0 ? s.bb : s.ba, SIDE, h);
+  if (h != start) {
+    bk.set_head(SIDE == 0 ? s.bb : s.ba, SIDE, h);
+    if (STATS) ++s.zruns;
+  }
   return ok;
 }
 
@@ -900,9 +924,36 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
   while (s.bb >= 0 && s.ba < L && s.bb >= s.ba) {
     if (s.bh >= (uint32_t)O || s.ah >= (uint32_t)O) break;  // NULL head (:155)
     if (passes++ >= budget || sink.full()) return false;
-    if (STATS) ++s.npass;
     // Records of heads that changed (the entry heads come from the prologue);
     // every size change is written through, so memory is current.
+    if constexpr (BookMem::kStaged) {
+      // On the staged book a read costs no memory traffic, so both head
+      // records and, when not read ahead yet, the next level's head of each
+      // side are read every pass, all issued before the first wait (the
+      // conditional reads below would each wait on their own).
+      if (!s.ahead) {
+        uint64_t t[W];
+#pragma unroll
+        for (int i = 0; i < W; ++i) t[i] = s.bm[i];
+        mask_clear<W>(t, s.bb);
+        s.pb = mask_highest<W>(t);
+#pragma unroll
+        for (int i = 0; i < W; ++i) t[i] = s.am[i];
+        mask_clear<W>(t, s.ba);
+        s.pa = mask_lowest<W>(t, L);
+      }
+      const uint4 br = bk.record(s.bh), ar = bk.record(s.ah);
+      const uint32_t pbh = bk.head(s.pb >= 0 ? s.pb : 0, 0);
+      const uint32_t pah = bk.head(s.pa < L ? s.pa : 0, 1);
+      s.brec = br;
+      s.arec = ar;
+      s.have_b = s.have_a = true;
+      if (!s.ahead) {
+        s.pbh = pbh;
+        s.pah = pah;
+        s.ahead = true;
+      }
+    }
     if (!s.have_b) {
       s.brec = bk.record(s.bh);
       s.have_b = true;
@@ -929,13 +980,16 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
     }
     // On the staged book a pass costs instructions, not memory round trips,
     // so the short zero-size walk pays there (in global memory it does not).
-    if (BookMem::kStaged && s.bh != s.ah) {
-      if ((int32_t)s.brec.x == 0 && (int32_t)s.arec.x > 0) {
-        if (!zero_walk<0>(s, c, bk, sink, out, budget, passes)) return false;
-      } else if ((int32_t)s.arec.x == 0 && (int32_t)s.brec.x > 0) {
-        if (!zero_walk<1>(s, c, bk, sink, out, budget, passes)) return false;
+    if constexpr (BookMem::kStaged) {
+      if (s.bh != s.ah) {
+        if ((int32_t)s.brec.x == 0 && (int32_t)s.arec.x > 0) {
+          if (!zero_walk<0, STATS>(s, c, bk, sink, out, budget, passes)) return false;
+        } else if ((int32_t)s.arec.x == 0 && (int32_t)s.brec.x > 0) {
+          if (!zero_walk<1, STATS>(s, c, bk, sink, out, budget, passes)) return false;
+        }
       }
     }
+    if (STATS) ++s.npass;
     const int32_t bsz = (int32_t)s.brec.x, asz = (int32_t)s.arec.x;
     const int32_t qty = bsz < asz ? bsz : asz;
     if (s.fc >= F) {  // overflow sentinel (:187-195)
@@ -1050,7 +1104,7 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
   int32_t obs = 0, oas = 0;
   if (kSizes && s.bb >= 0 && s.bh < (uint32_t)O) obs = s.have_b ? (int32_t)s.brec.x : bk.size(s.bh);
   if (kSizes && s.ba < L && s.ah < (uint32_t)O) oas = s.have_a ? (int32_t)s.arec.x : bk.size(s.ah);
-  out.counts[m] = s.fc;
+  gst(out.counts + m, s.fc);
   // (a multi-step launch keeps these in registers and stores them after its
   // last step only)
   const bool store = !MULTI || last || !Carry<W>::kState;
@@ -1106,6 +1160,8 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
     add_u64(b.stats + 5, (unsigned long long)s.npass);
     add_u64(b.stats + 6, (unsigned long long)(BookMem::kStaged ? 1 : 0));
     add_u64(b.stats + 7, (unsigned long long)(s.npass > 0 ? 1 : 0));
+    add_u64(b.stats + 8, (unsigned long long)s.zruns);
+    add_u64(b.stats + 9, (unsigned long long)s.zrows);
   }
 }
 
@@ -1215,7 +1271,6 @@ __device__ __forceinline__ void write_bulk_wave(const FillOut &out, const Bulk &
 // LDS per wavefront: the fill-row buffer during the first pass, then (when
 // staging is enabled for the shape) the staged book of one market.
 constexpr size_t kSinkBytesPerWave = 8 * kRows * 64 * sizeof(int32_t);
-constexpr size_t kMaxStageBytes = 32 * 1024;
 typedef __attribute__((address_space(1))) void gvoid_t;  // global memory
 typedef __attribute__((address_space(3))) void lvoid_t;  // LDS
 
@@ -1444,10 +1499,12 @@ template <int W, bool GAME, bool MULTI>
 int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &fo,
                        const StepOut &so, int32_t steps, hipStream_t s) {
   const Book b = book_of(h);
-  // Staging needs the market's records and level words in LDS next to the
-  // block's other wavefronts' buffers, within 64 KB per workgroup.
-  const bool staged = h->stage_budget > 0 && stage_bytes(h->L, h->O) <= kMaxStageBytes &&
-                      (size_t)(h->block / 64) * align_up(stage_bytes(h->L, h->O), 16) <= 65536;
+  // Staging needs each wavefront's copy of a book (its records, level words
+  // and row buffers) in LDS, within what a workgroup may use on the device
+  // (160 KB on gfx950).
+  const bool staged = h->stage_budget > 0 &&
+                      (size_t)(h->block / 64) * align_up(stage_bytes(h->L, h->O), 16) <=
+                          (size_t)h->lds_limit;
   const int32_t budget = staged ? h->stage_budget : 0x7FFFFFFF;
 #ifdef ASTRA_HOST_EMULATION
   (void)s;
@@ -1729,6 +1786,8 @@ int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, i
   ASTRA_ABI_CHECK(workspace_bytes, >=, lay.total);
   DeviceGuard g(device_id);
   if (!g.ok) return fail(ASTRA_ERR_HIP, "hipSetDevice failed");
+  int lds_limit = 0;
+  ASTRA_HIP_CHECK(rt_lds_per_block(device_id, &lds_limit), "hipDeviceGetAttribute");
   astra_market *h = new astra_market();
   h->M = M;
   h->L = L;
@@ -1741,6 +1800,7 @@ int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, i
   h->tid = 0;
   h->block = default_block();
   h->stage_budget = default_stage_budget();
+  h->lds_limit = lds_limit;
   h->per_wave = default_per_wave();
   h->stats = nullptr;
   h->ws = static_cast<char *>(workspace);

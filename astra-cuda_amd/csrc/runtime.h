@@ -36,6 +36,11 @@ inline hipError_t rt_memcpy(void *d, const void *s, size_t n, hipStream_t) {
 }
 inline hipError_t rt_sync(hipStream_t) { return hipSuccess; }
 inline hipError_t rt_last_error() { return hipSuccess; }
+// The host build stands in for gfx950, whose workgroups may use 160 KB of LDS.
+inline hipError_t rt_lds_per_block(int, int *bytes) {
+  *bytes = 160 * 1024;
+  return hipSuccess;
+}
 struct DeviceGuard {
   bool ok = true;
   explicit DeviceGuard(int) {}
@@ -52,6 +57,9 @@ inline hipError_t rt_memcpy(void *d, const void *s, size_t n, hipStream_t st) {
 }
 inline hipError_t rt_sync(hipStream_t st) { return hipStreamSynchronize(st); }
 inline hipError_t rt_last_error() { return hipGetLastError(); }
+inline hipError_t rt_lds_per_block(int dev, int *bytes) {
+  return hipDeviceGetAttribute(bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+}
 // Restores the calling thread's current device when it goes out of scope.
 struct DeviceGuard {
   int prev = -1;

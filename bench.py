@@ -7,10 +7,18 @@ through the hot path. Inputs are generated on the host by the deterministic
 counter-based generator (astra_cuda.workloads), uploaded, and resident in HBM
 before timing starts.
 
+The timed window is the END of the config's run: a config defines a run of
+``steps`` steps (config 3: 1,000, whose order ring wraps at step 512 and evicts
+from then on), and ``--warmup W --steps K`` time steps [S + W, S + W + K) with
+S = max(0, run steps - W - K). Steps [0, S) are a pre-roll through the same API,
+untimed, so a short run measures the book in the state the config defines (for
+config 3 the eviction regime) rather than an empty one. ``--start`` overrides S.
+The window is reported in ``config.timed_steps``.
+
 Phases (only A is the headline; B-D replay the same steps from clones of the
 pre-timed state, so they see exactly the same work):
-  A  throughput: W warm-up steps, then exactly K steps, no host sync inside,
-     bracketed by torch.cuda.synchronize() on both sides;
+  A  throughput: exactly K steps, no host sync inside, bracketed by
+     torch.cuda.synchronize() on both sides;
   B  latency: per-step host time with the stream synced (p50 / p99 / max);
   C  device time: HIP events on the launch stream around the K matching-kernel
      launches issued back to back (then around K get_bbos launches), so the
@@ -24,7 +32,8 @@ pre-timed state, so they see exactly the same work):
      (add_two_sided_quotes_steps, not in the reference; every step's BBOs kept),
      reported beside the headline under "multistep".
 Then the CPU baseline: the oracle (a C port of the reference algorithm) on a
-bounded subset of the same markets and steps, all host threads and 1 thread.
+bounded subset of the same markets, replaying the same pre-roll and warm-up
+untimed and timing the same window, on all host threads and on 1 thread.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -54,6 +63,9 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=900, help="timed steps K")
     ap.add_argument("--warmup", type=int, default=100, help="untimed warm-up steps W")
+    ap.add_argument("--start", type=int, default=None,
+                    help="untimed pre-roll steps S before the warm-up (default: the config's run "
+                         "length - W - K, so the timed steps are the last K of the run)")
     ap.add_argument("--config", type=int, default=3,
                     help="BASELINE.json config index (2, 3 or 4; 5 = the high-low game step; "
                          "6 = the reference's own game benchmark workload, "
@@ -90,6 +102,17 @@ def cpu_info():
     return model, avail
 
 
+def pre_roll(args, run_steps: int) -> int:
+    """Untimed steps before the warm-up: by default the timed steps are the last K
+    of the config's run (W + K past its end is allowed: the generator is defined
+    for every step)."""
+    if args.start is not None:
+        if args.start < 0:
+            raise SystemExit("--start must be >= 0")
+        return args.start
+    return max(0, run_steps - args.warmup - args.steps)
+
+
 def copy_calibration():
     import torch
     n = 1 << 30  # 1 GiB
@@ -124,7 +147,9 @@ def main():
     cfg = CONFIGS[args.config]
     M = args.markets or cfg.M
     W, K = args.warmup, args.steps
-    T = W + K
+    S = pre_roll(args, cfg.steps)
+    T0 = S + W          # first timed step
+    T = T0 + K
     bbo = cfg.bbo_every_step and not args.no_bbo
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -133,7 +158,8 @@ def main():
     t0 = time.perf_counter()
     qs = QuoteStream(cfg, np.arange(M))
     host = qs.steps(0, T)
-    log(f"generated config {cfg.index} inputs: {T} steps x {M} markets in {time.perf_counter() - t0:.1f}s")
+    log(f"generated config {cfg.index} inputs: {T} steps x {M} markets in {time.perf_counter() - t0:.1f}s; "
+        f"timed steps [{T0}, {T})")
     dev_in = [torch.from_numpy(a).to(dev) for a in host]
     rows = [tuple(x[t] for x in dev_in) for t in range(T)]
     torch.cuda.synchronize()
@@ -149,19 +175,19 @@ def main():
         if bbo:
             mk.get_bbos(bbos)
 
-    for t in range(W):
+    for t in range(T0):
         step(market, t)
     torch.cuda.synchronize()
     phases = set(args.phases.upper()) | {"A"}
     # state at the start of the timed steps, for the replays B, C and D
     snaps = [market.clone() if p in phases else None for p in "BCDRS"]
     torch.cuda.synchronize()
-    log(f"warm-up done ({W} steps); timing {K} steps")
+    log(f"pre-roll ({S} steps) and warm-up ({W} steps) done; timing {K} steps")
 
     # ---- A: throughput (the headline) ----
     torch.cuda.synchronize()
     a0 = time.perf_counter()
-    for t in range(W, T):
+    for t in range(T0, T):
         step(market, t)
     torch.cuda.synchronize()
     wall = time.perf_counter() - a0
@@ -172,7 +198,7 @@ def main():
     lat = [float("nan")]
     if nlat:
         lat = []
-    for t in range(W, W + nlat):
+    for t in range(T0, T0 + nlat):
         torch.cuda.synchronize()
         h0 = time.perf_counter()
         step(snaps[0], t)
@@ -189,11 +215,11 @@ def main():
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         torch.cuda.synchronize()
         ev[0].record()
-        for t in range(W, T):
+        for t in range(T0, T):
             snaps[1].add_two_sided_quotes(*rows[t], fills)
         ev[1].record()
         if bbo:
-            for t in range(W, T):
+            for t in range(T0, T):
                 snaps[1].get_bbos(bbos)
         ev[2].record()
         torch.cuda.synchronize()
@@ -202,14 +228,15 @@ def main():
             bbo_ms = np.array([ev[1].elapsed_time(ev[2]) / K])
 
     # ---- D: exact work counts for the algorithmic bytes ----
-    counters = torch.zeros(8, dtype=torch.int64, device=dev)
+    counters = torch.zeros(10, dtype=torch.int64, device=dev)
     if "D" in phases:
         snaps[2]._set_stats(counters)
-        for t in range(W, T):
+        for t in range(T0, T):
             snaps[2].add_two_sided_quotes(*rows[t], fills)
         torch.cuda.synchronize()
         snaps[2]._set_stats(None)
-    n_ins, n_fill, n_empty, n_ovf, n_ff, n_pass, n_staged, n_cross = (int(x) for x in counters.cpu().tolist())
+    (n_ins, n_fill, n_empty, n_ovf, n_ff, n_pass, n_staged, n_cross, n_zruns,
+     n_zrows) = (int(x) for x in counters.cpu().tolist())
 
     # ---- R: the same steps with the row layout of the FillBatch ----
     wall_rows = None
@@ -217,7 +244,7 @@ def main():
         rfills = snaps[3].new_fill_batch(layout="rows")
         torch.cuda.synchronize()
         r0 = time.perf_counter()
-        for t in range(W, T):
+        for t in range(T0, T):
             snaps[3].add_two_sided_quotes(*rows[t], rfills)
             if bbo:
                 snaps[3].get_bbos(bbos)
@@ -229,7 +256,7 @@ def main():
     multistep = None
     if "S" in phases:
         step_bbos = torch.empty((4, K, M), dtype=torch.int32, device=dev) if bbo else None
-        ins = [x[W:T] for x in dev_in]
+        ins = [x[T0:T] for x in dev_in]
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
 
         def one_launch(mk, layout):
@@ -260,7 +287,7 @@ def main():
     qm_avg_s = float(qm_ms.mean()) * 1e-3
     achieved = qm_bytes / qm_avg_s / 1e9
 
-    traffic, traffic_src = measured_traffic(cfg, M, bbo)
+    traffic, traffic_src = measured_traffic(cfg, M, bbo, (T0, T))
     value = M * K / wall
     result = {
         "metric": "quote-matches/sec and market-steps/sec at 100k markets; p50 step latency",
@@ -279,7 +306,8 @@ def main():
             "workload": f"config{cfg.index}_{cfg.name}",
             "num_markets": M, "max_price_levels": cfg.L, "max_active_orders_per_market": cfg.O,
             "max_active_fills_per_market": cfg.F, "num_customers": cfg.C,
-            "get_bbos_every_step": bbo, "parallelism": "single GPU, one lane per market",
+            "get_bbos_every_step": bbo, "run_steps": cfg.steps, "pre_roll_steps": S,
+            "timed_steps": [T0, T], "parallelism": "single GPU, one lane per market",
         },
         "market_steps_per_s": K / wall,
         "value_rows_layout": (M * K / wall_rows) if wall_rows else None,
@@ -290,7 +318,8 @@ def main():
         "device_ms_per_step": {"quote_match": float(qm_ms.mean()), "get_bbos": float(bbo_ms.mean())},
         "work_per_step": {"inserts": n_ins / K, "fill_rows": n_fill / K, "levels_emptied": n_empty / K,
                           "overflow_markets": n_ovf / K, "crossing_markets": n_cross / K,
-                          "loop_passes": n_pass / K, "staged_markets": n_staged / K},
+                          "loop_passes": n_pass / K, "staged_markets": n_staged / K,
+                          "staged_zero_runs": n_zruns / K, "staged_zero_rows": n_zrows / K},
         "roofline": {
             "kernel": "quote_match_kernel",
             "bound": "hbm",
@@ -307,7 +336,7 @@ def main():
 
     # ---- CPU baseline: the oracle on a bounded subset of the same workload ----
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args, cfg, host, M, W, K, bbo)
+        result["cpu_baseline"] = cpu_baseline(args, cfg, host, M, T0, K, bbo)
     print(json.dumps(result), flush=True)
 
 
@@ -315,8 +344,9 @@ def bench_game(args):
     """Config 5: one trading move of every env of the high-low game per step
     (HighLowTradingState::ApplyPlayerTrading: AddTwoSidedQuotes, GetBBOs,
     UpdateLastPrices and the per-player rewards and telemetry). The chance moves
-    are applied before timing; the timed steps are trading moves W..W+K-1 of one
-    game (W + K <= players * steps_per_player)."""
+    are applied before timing; the timed steps are the last K trading moves of
+    one game, after S = players * steps_per_player - W - K untimed moves and W
+    warm-up moves (--start sets S; S + W + K must not exceed the game)."""
     import numpy as np
     import torch
     import astra_cuda as astra
@@ -327,8 +357,10 @@ def bench_game(args):
     P = cfg.players
     moves_total = P * cfg.steps_per_player
     W, K = args.warmup, args.steps
-    if W + K > moves_total:
-        print(f"config 5 has {moves_total} trading moves: warmup + steps must not exceed it",
+    S = pre_roll(args, moves_total)
+    T0 = S + W
+    if T0 + K > moves_total:
+        print(f"config 5 has {moves_total} trading moves: start + warmup + steps must not exceed it",
               file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda", 0)
@@ -336,28 +368,29 @@ def bench_game(args):
     t0 = time.perf_counter()
     gs = GameStream(cfg, np.arange(N))
     chance = gs.chance()
-    host_moves = [gs.move(k) for k in range(W + K)]
+    host_moves = [gs.move(k) for k in range(T0 + K)]
     moves = [torch.from_numpy(m).to(dev) for m in host_moves]
     chance_d = [torch.from_numpy(c).to(dev) for c in chance]
     torch.cuda.synchronize()
-    log(f"generated config 5 moves: {W + K} moves x {N} envs in {time.perf_counter() - t0:.1f}s")
+    log(f"generated config 5 moves: {T0 + K} moves x {N} envs in {time.perf_counter() - t0:.1f}s; "
+        f"timed moves [{T0}, {T0 + K})")
     astra.register_games()
     game = astra.load_game("high_low_trading", cfg.game_params(N, check_moves=True))
     state = game.new_initial_state()
     for c in chance_d:
         state.apply_action(c)
-    for k in range(W):
+    for k in range(T0):
         state.apply_action(moves[k])
     torch.cuda.synchronize()
     snaps = [state.clone() for _ in range(4)]
     torch.cuda.synchronize()
-    log(f"warm-up done ({W} moves); timing {K} moves")
+    log(f"pre-roll ({S} moves) and warm-up ({W} moves) done; timing {K} moves")
 
     def timed(st, check):
         st.set_check_moves(check)
         torch.cuda.synchronize()
         a0 = time.perf_counter()
-        for k in range(W, W + K):
+        for k in range(T0, T0 + K):
             st.apply_action(moves[k])
         torch.cuda.synchronize()
         return time.perf_counter() - a0
@@ -368,7 +401,7 @@ def bench_game(args):
     # B: per-move latency, checked
     st = snaps[1]
     lat = []
-    for k in range(W, W + min(K, args.latency_steps)):
+    for k in range(T0, T0 + min(K, args.latency_steps)):
         torch.cuda.synchronize()
         h0 = time.perf_counter()
         st.apply_action(moves[k])
@@ -381,7 +414,7 @@ def bench_game(args):
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     torch.cuda.synchronize()
     ev[0].record()
-    for k in range(W, W + K):
+    for k in range(T0, T0 + K):
         st.apply_action(moves[k])
     ev[1].record()
     torch.cuda.synchronize()
@@ -389,9 +422,9 @@ def bench_game(args):
     # D: work counts of the matching kernel
     st = snaps[3]
     st.set_check_moves(False)
-    counters = torch.zeros(8, dtype=torch.int64, device=dev)
+    counters = torch.zeros(10, dtype=torch.int64, device=dev)
     st.market._set_stats(counters)
-    for k in range(W, W + K):
+    for k in range(T0, T0 + K):
         st.apply_action(moves[k])
     torch.cuda.synchronize()
     st.market._set_stats(None)
@@ -405,7 +438,7 @@ def bench_game(args):
     game_bytes = N * ((16 + 4 + 4 + 16 * P) + (16 + 4 + 28 + 24 * P))
     step_bytes = (24.0 * N * K + 32.0 * n_ins + 109.0 * n_fill + 8.0 * n_empty) / K + game_bytes
     achieved = step_bytes / (step_ms * 1e-3) / 1e9
-    traffic, traffic_src = game_traffic(cfg, N)
+    traffic, traffic_src = game_traffic(cfg, N, (T0, T0 + K))
     result = {
         "metric": "quote-matches/sec and market-steps/sec at 100k markets; p50 step latency",
         "value": N * K / wall,
@@ -424,6 +457,7 @@ def bench_game(args):
             "steps_per_player": cfg.steps_per_player, "max_contract_value": cfg.max_contract_value,
             "max_contracts_per_trade": cfg.max_contracts_per_trade,
             "market_shape_LOFC": list(cfg.market_shape), "move_checks": "one host wait per move (for the checks)",
+            "run_moves": moves_total, "pre_roll_moves": S, "timed_moves": [T0, T0 + K],
             "parallelism": "single GPU, one lane per env",
         },
         "market_steps_per_s": K / wall,
@@ -440,7 +474,7 @@ def bench_game(args):
         },
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = game_cpu_baseline(args, cfg, chance, host_moves, N, W, K)
+        result["cpu_baseline"] = game_cpu_baseline(args, cfg, chance, host_moves, N, T0, K)
     print(json.dumps(result), flush=True)
 
 
@@ -542,39 +576,47 @@ def bench_game_reference(args):
     print(json.dumps(result), flush=True)
 
 
-def game_cpu_baseline(args, cfg, chance, host_moves, N, W, K):
+def game_cpu_baseline(args, cfg, chance, host_moves, N, T0, K):
     """The game oracle (numpy state operations over the C market oracle, one
-    thread) on the first envs of the same stream."""
+    thread) on the first envs of the same stream: the same untimed moves [0, T0),
+    then the timed moves [T0, T0 + K)."""
     import numpy as np
     from oracle.high_low_oracle import OracleHighLow
 
     model, avail = cpu_info()
 
-    def run(n, steps):
+    def run(n, pre, steps):
         o = OracleHighLow(n, cfg.players, cfg.steps_per_player, cfg.max_contracts_per_trade,
                           cfg.customer_max_size, cfg.max_contract_value, market_shape=cfg.market_shape)
         for c in chance:
             o.apply_action(np.ascontiguousarray(c[:n]))
-        for k in range(W):
+        for k in range(pre):
             o.apply_action(np.ascontiguousarray(host_moves[k][:n]))
         c0 = time.perf_counter()
-        for k in range(W, W + steps):
+        for k in range(pre, pre + steps):
             o.apply_action(np.ascontiguousarray(host_moves[k][:n]))
         return n * steps / (time.perf_counter() - c0)
 
-    rate = run(min(N, 1000), min(K, 50))
-    n = int(min(N, max(500, rate * args.cpu_seconds / K)))
-    log(f"CPU leg: {n} envs x {K} moves")
-    v = run(n, K)
+    n0 = min(N, 1000)
+    rate = run(n0, 0, min(T0 + K, 50))
+    # envs such that the untimed moves and the timed window together take about
+    # cpu_seconds
+    n = int(min(N, max(500, rate * args.cpu_seconds / (T0 + K))))
+    log(f"CPU leg: {n} envs, {T0} untimed + {K} timed moves")
+    v = run(n, T0, K)
     return {"value": v, "unit": "quote-matches/s", "cores": 1, "kind": "port",
-            "sample": f"envs 0..{n - 1} of the same config-5 stream, the same {W} warm-up + {K} timed moves",
+            "sample": f"envs 0..{n - 1} of the same config-5 stream: moves [0, {T0}) untimed, "
+                      f"the timed moves [{T0}, {T0 + K})",
             "host_cpu": model, "host_cpus_available": avail}
 
 
-def profile_traffic(profile: str, kernel: str):
-    """HBM bytes per launch of `kernel` from a committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary under profiles/ (copy-calibrated), or (None, None)."""
-    key = f"traffic_bytes_per_launch[void {kernel}]:"
+def profile_traffic(profile: str, kernel: str, window):
+    """HBM bytes per launch of `kernel` over the launches of steps [window) from a
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/
+    (copy-calibrated), or (None, None) when the summary holds no figure for
+    exactly that window (traffic depends on the book's state, so a figure from
+    other steps would describe other work)."""
+    key = f"traffic_bytes_per_launch[void {kernel}][{window[0]},{window[1]}]:"
     path = os.path.join(ROOT, "profiles", profile)
     try:
         with open(path) as f:
@@ -586,64 +628,86 @@ def profile_traffic(profile: str, kernel: str):
     return None, None
 
 
-def measured_traffic(cfg, M, bbo):
-    """HBM bytes per matching-kernel launch for this workload (see profile_traffic)."""
+def measured_traffic(cfg, M, bbo, window):
+    """HBM bytes per matching-kernel launch for this workload and window (see
+    profile_traffic)."""
     if M != cfg.M or bbo != cfg.bbo_every_step:
         return None, None
     words = 1
     while words * 64 < cfg.L:
         words *= 2
     return profile_traffic(f"quote_match_config{cfg.index}_{cfg.name}_hbm_traffic.md",
-                           f"quote_match_kernel<{words}, false, false, false, false>")
+                           f"quote_match_kernel<{words}, false, false, false, false>", window)
 
 
-def game_traffic(cfg, N):
-    """HBM bytes per fused game-move launch for this workload (see profile_traffic)."""
+def game_traffic(cfg, N, window):
+    """HBM bytes per fused game-move launch for this workload and window (see
+    profile_traffic)."""
     if N != cfg.envs:
         return None, None
     return profile_traffic(f"game_move_config5_{cfg.name}_kernel_trace.md",
-                           "quote_match_kernel<2, false, true, false, true>")
+                           "quote_match_kernel<2, false, true, false, true>", window)
 
 
-def cpu_baseline(args, cfg, host, M, W, K, bbo):
+def cpu_baseline(args, cfg, host, M, T0, K, bbo):
+    """The C oracle on markets [0, mc) of the same stream: steps [0, T0) untimed,
+    then the timed window [T0, T0 + K) on all host threads; then, from a copy of
+    the state at T0, the first steps of the window on one thread."""
     import numpy as np
     from oracle.oracle import OracleMarket
 
     model, avail = cpu_info()
-    nthreads = max(1, min(avail, 16))
+    nthreads = max(1, avail)
 
-    def run(mc, threads, steps_timed):
-        o = OracleMarket(mc, cfg.L, cfg.O, cfg.F, cfg.C)
-        f = o.new_fill_batch()
-        b = o.new_bbo_batch()
-        sl = [np.ascontiguousarray(a[:, :mc]) for a in host]
-        for t in range(W):
+    def sliced(mc):
+        return [np.ascontiguousarray(a[:, :mc]) for a in host]
+
+    def steps(o, f, b, sl, t0, t1, threads, with_bbo):
+        for t in range(t0, t1):
             o.add_two_sided_quotes(*(a[t] for a in sl), f, nthreads=threads)
-        c0 = time.perf_counter()
-        for t in range(W, W + steps_timed):
-            o.add_two_sided_quotes(*(a[t] for a in sl), f, nthreads=threads)
-            if bbo:
+            if with_bbo:
                 o.get_bbos(b, nthreads=threads)
-        return mc * steps_timed / (time.perf_counter() - c0)
 
-    # calibrate on a small sample, then size each leg to a bounded CPU time
-    rate_all = run(min(M, 2000), nthreads, min(K, 50))
-    mc_all = int(min(M, max(1000, rate_all * args.cpu_seconds / K)))
-    log(f"CPU leg: {mc_all} markets x {K} timed steps on {nthreads} threads")
-    v_all = run(mc_all, nthreads, K)
-    rate_one = run(min(M, 500), 1, min(K, 50))
-    mc_one = int(min(M, max(200, rate_one * (args.cpu_seconds / 3) / K)))
-    log(f"CPU leg: {mc_one} markets x {K} timed steps on 1 thread")
-    v_one = run(mc_one, 1, K)
+    # calibrate on a small sample, then size the sample so that the untimed steps
+    # and the window together take about cpu_seconds on all threads
+    mc0 = min(M, 2000)
+    o = OracleMarket(mc0, cfg.L, cfg.O, cfg.F, cfg.C)
+    f, b = o.new_fill_batch(), o.new_bbo_batch()
+    n0 = min(T0 + K, 50)
+    c0 = time.perf_counter()
+    steps(o, f, b, sliced(mc0), 0, n0, nthreads, bbo)
+    rate = mc0 * n0 / (time.perf_counter() - c0)
+    del o, f, b
+    mc = int(min(M, max(1000, rate * args.cpu_seconds / (T0 + K))))
+    log(f"CPU leg: {mc} markets, {T0} untimed + {K} timed steps on {nthreads} threads")
+    sl = sliced(mc)
+    o = OracleMarket(mc, cfg.L, cfg.O, cfg.F, cfg.C)
+    f, b = o.new_fill_batch(), o.new_bbo_batch()
+    steps(o, f, b, sl, 0, T0, nthreads, False)  # get_bbos changes no state
+    o1 = o.clone()
+    c0 = time.perf_counter()
+    steps(o, f, b, sl, T0, T0 + K, nthreads, bbo)
+    v_all = mc * K / (time.perf_counter() - c0)
+    del o
+    # one thread: window steps one at a time until a third of cpu_seconds is spent
+    k1, spent = 0, 0.0
+    while k1 < K and spent < args.cpu_seconds / 3:
+        c0 = time.perf_counter()
+        steps(o1, f, b, sl, T0 + k1, T0 + k1 + 1, 1, bbo)
+        spent += time.perf_counter() - c0
+        k1 += 1
+    v_one = mc * k1 / spent
+    log(f"CPU leg: {mc} markets x {k1} steps on 1 thread")
     return {
         "value": v_all,
         "unit": "quote-matches/s",
         "cores": nthreads,
         "kind": "port",
-        "sample": (f"markets 0..{mc_all - 1} of the same config-{cfg.index} stream, the same "
-                   f"{W} warm-up + {K} timed steps" + (" with get_bbos every step" if bbo else "")),
+        "sample": (f"markets 0..{mc - 1} of the same config-{cfg.index} stream: steps [0, {T0}) "
+                   f"untimed, the timed steps [{T0}, {T0 + K})"
+                   + (" with get_bbos every step" if bbo else "")),
         "single_thread_value": v_one,
-        "single_thread_sample": f"markets 0..{mc_one - 1}, same steps",
+        "single_thread_sample": f"markets 0..{mc - 1}, timed steps [{T0}, {T0 + k1})",
         "host_cpu": model,
         "host_cpus_available": avail,
     }

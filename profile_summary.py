@@ -1,8 +1,8 @@
 """Reduce rocprofv3 CSV output of a bench.py run to the figures the bench reports.
 
-    python -m astra_cuda.profile_summary trace  <dir> [--blocks 100,900,300,900]
-    python -m astra_cuda.profile_summary pmc    <dir> [--skip 100 --take 900]
-    python -m astra_cuda.profile_summary traffic <fetch dir> <write dir> \
+    python3 profile_summary.py trace  <dir> [--blocks 100,900,300,900]
+    python3 profile_summary.py pmc    <dir> [--skip 100 --take 900]
+    python3 profile_summary.py traffic <fetch dir> <write dir> \
         <copy fetch dir> <copy write dir> [--skip 100 --take 900]
 
 ``trace`` reads ``*_kernel_stats.csv`` / ``*_kernel_trace.csv`` of a
@@ -13,7 +13,11 @@ matching-kernel launches as warm-up W, timed K, latency replay, event replay).
 ``traffic`` turns FETCH_SIZE and WRITE_SIZE (KiB per dispatch) into HBM bytes per
 launch, each scaled by what the same counter reads for bench.py's
 ``--copy-calibration`` run (a 1 GiB device copy): bytes = KiB * 1024 * (2^30 /
-copy KiB * 1024). Output is markdown on stdout.
+copy KiB * 1024). Output is markdown on stdout. Means are over dispatches
+[skip, skip + take) of each kernel; with ``bench.py --phases A`` the matching
+kernel's dispatch d is step d, so the window is the bench's ``timed_steps``, and
+the ``traffic_bytes_per_launch[kernel][first,end]`` lines that bench.py reads
+carry it.
 """
 from __future__ import annotations
 
@@ -121,7 +125,7 @@ def traffic(fetch: str, write: str, cfetch: str, cwrite: str, skip: int, take: i
         rb, wb = f * 1024 * f_fac, w * 1024 * w_fac
         out.append(f"| `{k}` | {len(fc[k]['FETCH_SIZE'])} | {f:.1f} | {w:.1f} | {rb:.4g} | {wb:.4g} | "
                    f"{rb + wb:.4g} |")
-        lines.append(f"traffic_bytes_per_launch[{k}]: {rb + wb:.0f}")
+        lines.append(f"traffic_bytes_per_launch[{k}][{skip},{skip + take}]: {rb + wb:.0f}")
     return "\n".join(out + [""] + lines)
 
 

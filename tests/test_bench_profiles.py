@@ -1,8 +1,10 @@
 """bench.py reads `roofline.traffic` from the committed rocprofv3 summaries under
-profiles/ by kernel name: the names it asks for must be the ones those summaries
-hold (a kernel's template arguments are part of its name). CPU only."""
+profiles/ by kernel name and step window: the names it asks for must be the ones
+those summaries hold (a kernel's template arguments are part of its name), and
+a figure is used only for exactly the steps it was measured on. CPU only."""
 import os
 import sys
+import types
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, ROOT)
@@ -10,21 +12,39 @@ sys.path.insert(0, ROOT)
 import bench  # noqa: E402  (stdlib imports only at module level)
 from astra_cuda.workloads import CONFIGS, GAME_CONFIG  # noqa: E402
 
+# the driver's command: bench.py --steps 20 --warmup 5
+DRIVER = types.SimpleNamespace(start=None, warmup=5, steps=20)
 
-def test_matching_kernel_traffic_is_found_for_config3():
+
+def _window(run_steps):
+    t0 = bench.pre_roll(DRIVER, run_steps) + DRIVER.warmup
+    return (t0, t0 + DRIVER.steps)
+
+
+def test_driver_window_is_the_end_of_the_run():
+    assert _window(CONFIGS[3].steps) == (980, 1000)   # config 3: ring wrapped at step 512
+    default = types.SimpleNamespace(start=None, warmup=100, steps=900)
+    assert bench.pre_roll(default, CONFIGS[3].steps) == 0
+    assert bench.pre_roll(types.SimpleNamespace(start=7, warmup=5, steps=20), 1000) == 7
+
+
+def test_matching_kernel_traffic_is_found_for_config3_driver_window():
     cfg = CONFIGS[3]
-    traffic, src = bench.measured_traffic(cfg, cfg.M, cfg.bbo_every_step)
+    traffic, src = bench.measured_traffic(cfg, cfg.M, cfg.bbo_every_step, _window(cfg.steps))
     assert src == "profiles/quote_match_config3_stress_100k_hbm_traffic.md"
     assert traffic is not None and traffic > 0
 
 
-def test_game_move_traffic_is_found_for_config5():
-    traffic, src = bench.game_traffic(GAME_CONFIG, GAME_CONFIG.envs)
+def test_game_move_traffic_is_found_for_config5_driver_window():
+    moves = GAME_CONFIG.players * GAME_CONFIG.steps_per_player
+    traffic, src = bench.game_traffic(GAME_CONFIG, GAME_CONFIG.envs, _window(moves))
     assert src == "profiles/game_move_config5_game_step_10k_kernel_trace.md"
     assert traffic is not None and traffic > 0
 
 
-def test_other_workloads_report_no_traffic():
+def test_other_workloads_and_windows_report_no_traffic():
     cfg = CONFIGS[3]
-    assert bench.measured_traffic(cfg, cfg.M // 2, cfg.bbo_every_step) == (None, None)
-    assert bench.game_traffic(GAME_CONFIG, GAME_CONFIG.envs + 1) == (None, None)
+    w = _window(cfg.steps)
+    assert bench.measured_traffic(cfg, cfg.M // 2, cfg.bbo_every_step, w) == (None, None)
+    assert bench.measured_traffic(cfg, cfg.M, cfg.bbo_every_step, (5, 25)) == (None, None)
+    assert bench.game_traffic(GAME_CONFIG, GAME_CONFIG.envs + 1, w) == (None, None)

@@ -38,27 +38,30 @@ def _compare(em, ef, eb, om, of, ob, F, where):
     assert np.array_equal(em.portfolios, om.customer_portfolios), where
 
 
-def _emu(M, L, O, F, C, stage_budget=None):
+def _emu(M, L, O, F, C, stage_budget=None, extended=None):
     """Emulated engine; stage_budget sets the passes before a market's book is staged
     (0: never), read by the engine when the market is created."""
-    if stage_budget is None:
-        return EmuMarket(M, L, O, F, C)
-    old = os.environ.get("ASTRA_MARKET_STAGE_BUDGET")
-    os.environ["ASTRA_MARKET_STAGE_BUDGET"] = str(stage_budget)
+    env = {"ASTRA_MARKET_STAGE_BUDGET": stage_budget}
+    old = {k: os.environ.get(k) for k in env}
     try:
-        return EmuMarket(M, L, O, F, C)
+        for k, v in env.items():
+            if v is not None:
+                os.environ[k] = str(v)
+        return EmuMarket(M, L, O, F, C, extended=extended)
     finally:
-        if old is None:
-            del os.environ["ASTRA_MARKET_STAGE_BUDGET"]
-        else:
-            os.environ["ASTRA_MARKET_STAGE_BUDGET"] = old
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
 
 
-def _run(M, L, O, F, C, steps, gen, with_stats=False, stage_budget=None, layout="columns"):
-    em, om = _emu(M, L, O, F, C, stage_budget), OracleMarket(M, L, O, F, C)
+def _run(M, L, O, F, C, steps, gen, with_stats=False, stage_budget=None, layout="columns",
+         extended=None):
+    em, om = _emu(M, L, O, F, C, stage_budget, extended), OracleMarket(M, L, O, F, C)
     ef, of = em.new_fill_batch(layout), om.new_fill_batch()
     eb, ob = em.new_bbo_batch(), om.new_bbo_batch()
-    stats = np.zeros(8, np.int64)
+    stats = np.zeros(10, np.int64)
     ostats = {"inserts": 0, "fills": 0, "levels_emptied": 0, "overflows": 0}
     if with_stats:
         em.set_stats(stats)
@@ -78,7 +81,11 @@ def _run(M, L, O, F, C, steps, gen, with_stats=False, stage_budget=None, layout=
         assert stats.tolist()[:4] == [ostats["inserts"], ostats["fills"], ostats["levels_emptied"],
                                       ostats["overflows"]]
         ostats["fast_forwards"] = int(stats[4])
+        ostats["staged"] = int(stats[6])
+        ostats["zero_runs"] = int(stats[8])
+        ostats["zero_rows"] = int(stats[9])
     assert em.global_tid == om.global_tid
+    ostats["last_fills"] = of
     return em, om, ostats
 
 
@@ -205,3 +212,44 @@ def test_emulated_zero_sized_shapes():
     b = em.new_bbo_batch()
     em.get_bbos(b)
     assert f.fill_counts.tolist() == [0, 0, 0] and b.best_bid_prices.tolist() == [-1, -1, -1]
+
+
+# Markets of the config-3 stream whose books, after the order ring wraps, walk long
+# runs of zero-size fills (consumed orders that slot reuse has linked into live
+# lists): at O = 1024 runs of up to about 110 rows, and market 115 at O = F = 4096
+# (extended shape) a run of 631 rows at step 2457, which spans ten flushes of the
+# staged walk's 64-row buffer.
+LONG_WALK_MARKETS = [115, 21099, 72837, 22178, 66430, 46789, 23615, 89995, 93998, 90015]
+
+
+@pytest.mark.parametrize("stage_budget", [None, 1, 3, 0])
+def test_emulated_zero_size_runs_after_the_wrap(stage_budget):
+    """The config-3 stream past the ring wrap against the oracle, with markets
+    staged after the default number of passes, after 1 and 3, and never."""
+    from astra_cuda.workloads import CONFIGS, QuoteStream
+    cfg = CONFIGS[3]
+    qs = QuoteStream(cfg, np.array(LONG_WALK_MARKETS + list(range(54)), np.int64))
+    M = len(LONG_WALK_MARKETS) + 54
+    _, _, st = _run(M, cfg.L, cfg.O, cfg.F, cfg.C, cfg.steps, qs.step, with_stats=True,
+                    stage_budget=stage_budget)
+    if stage_budget == 0:
+        assert st["staged"] == 0 and st["zero_runs"] == 0
+    else:
+        assert st["zero_runs"] > 20 and st["zero_rows"] > 3 * st["zero_runs"]
+
+
+def test_emulated_zero_size_run_of_631_rows():
+    from astra_cuda.workloads import CONFIGS, QuoteStream
+    cfg = CONFIGS[3]
+    O = F = 4096
+    qs = QuoteStream(cfg, np.array([115, 0, 1, 2], np.int64))
+    _, _, st = _run(4, cfg.L, O, F, cfg.C, 2458, qs.step, with_stats=True)
+    # the last step's rows of market 0 (stream market 115), compared above, hold the run
+    of = st["last_fills"]
+    n = int(of.fill_counts[0])
+    run = best = 0
+    for v in of.fill_sizes[0, :n]:
+        run = run + 1 if v == 0 else 0
+        best = max(best, run)
+    assert best == 631
+    assert st["zero_rows"] >= 631

@@ -157,6 +157,14 @@ def test_gpu_move_checks():
     with pytest.raises(RuntimeError, match="ask_sizes <= max_contracts_per_trade"):
         s2.check_errors()
     s2.check_errors()  # cleared
+    # a failed unchecked move, then checks switched on: the switch reports it and
+    # clears the word, so the next good checked move goes through
+    s2.apply_action(_t(bad))
+    with pytest.raises(RuntimeError, match="ask_sizes <= max_contracts_per_trade"):
+        s2.set_check_moves(True)
+    mv = s2.move_number()
+    s2.apply_action(_t(np.tile(np.array([[12, 18, 2, 1]], np.int32), (5, 1))))
+    assert s2.move_number() == mv + 1
 
 
 def test_gpu_move_checks_many_blocks():

@@ -104,3 +104,21 @@ def test_oracle_reset_replays_identically():
     assert not o.market.customer_portfolios.any() and o.market.global_tid == 0
     assert _play_hand(o) == first
     assert np.array_equal(o.fill_returns(), ret)
+
+
+def test_game_keeps_the_reference_market_caps():
+    """A game whose derived market exceeds the reference's VecMarket caps
+    (max_contract_value = 200 gives 201 price levels; market.cu:338-342) raises the
+    reference's constructor error, as the reference's game does; the non-reference
+    parameter market_extended_shapes lifts the caps (the constructor then gets as
+    far as the device check, since this test runs without a GPU)."""
+    import pytest
+    import astra_cuda as astra
+    astra.register_games()
+    prm = dict(num_markets=4, players=5, steps_per_player=2, max_contract_value=200)
+    with pytest.raises(RuntimeError, match="L <= ASTRA_PRICE_LEVELS"):
+        astra.load_game("high_low_trading", prm).new_initial_state()
+    import torch
+    if torch.cuda.device_count() == 0:
+        with pytest.raises(RuntimeError, match="device_id < device_count"):
+            astra.load_game("high_low_trading", dict(prm, market_extended_shapes=True)).new_initial_state()
