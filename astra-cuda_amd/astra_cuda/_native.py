@@ -43,6 +43,7 @@ PROTOTYPES = {
     "astra_market_set_tid": (_c_int, [_vp, _c_i32]),
     "astra_market_shape": (_c_int, [_vp] + [ctypes.POINTER(_c_i32)] * 5),
     "astra_high_low_trade": (_c_int, [_vp, _vp, _vp]),
+    "astra_high_low_trade_scratch": (_c_int, [_vp, _vp, _vp]),
     "astra_high_low_observation": (_c_int, [_vp, _vp]),
     "astra_high_low_rewards": (_c_int, [_vp, ctypes.c_int64, _c_i32, _c_i32, _vp, _vp]),
 }

@@ -170,6 +170,8 @@ class HighLowTradingState:
         # the checked move's error word lands here (pinned) for the one host wait
         self._errors_host = torch.zeros((1,), dtype=torch.int32, pin_memory=True)
         self._lib = _native.lib()
+        # the C entry point of a trading move (astra_high_low_trade)
+        self._trade_fn = self._lib.astra_high_low_trade
         self._trade = self._make_trade_args()
 
     @property
@@ -345,7 +347,7 @@ class HighLowTradingState:
         t.move = move.data_ptr()
         t.player = player
         t.trade_move_number = tmn
-        rc = self._lib.astra_high_low_trade(self.market._h, ctypes.byref(t),
+        rc = self._trade_fn(self.market._h, ctypes.byref(t),
                                            _raw_stream(self._game.device_id))
         self._last_move = move  # keep the buffer alive while the kernels may read it
         if rc:

@@ -15,6 +15,7 @@
 // The kernel bodies are __host__ __device__ functions; the host-emulation build
 // (-DASTRA_HOST_EMULATION) runs them as loops over host memory.
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "astra_high_low.h"
@@ -260,11 +261,59 @@ const char *check_text(int32_t bits) {  // the first failed check, as the refere
 
 }  // namespace
 
-extern "C" {
+// The error word of astra_high_low_trade_scratch: the library's own device
+// memory, so that its callers need not allocate any. Each GPU holds its own copy
+// at its own address (kept per device in g_scratch after hipGetSymbolAddress);
+// in host code the array's name is not a device address and is never used as
+// one. Word 0 holds the failed checks' bits of the call in flight; the other
+// words are unused. Every call on a GPU shares that GPU's copy.
+constexpr int kScratchWords = 64;
+#ifdef ASTRA_HOST_EMULATION
+static int32_t scratch[kScratchWords];  // the host build keeps its "device" memory on the host
+#else
+static __device__ __align__(256) int32_t scratch[kScratchWords];
+#endif
 
-int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *stream) {
-  ASTRA_ABI_CHECK(market != nullptr, ==, true);
-  ASTRA_ABI_CHECK(t != nullptr, ==, true);
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+struct ScratchDevice {
+  int32_t *ptr = nullptr;   // device address of `scratch` on this device
+  hipEvent_t ev = nullptr;  // the checks' completion event of this device
+};
+ScratchDevice g_scratch[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// Set-up, once per device with that device current: the address of its copy of
+// `scratch` and an event, so the calls themselves allocate nothing.
+int scratch_device(int dev, ScratchDevice **out) {
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(ASTRA_ERR_INVALID_ARGUMENT, "astra_high_low_trade_scratch: device id out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchDevice &d = g_scratch[dev];
+  if (!d.ptr) {
+#ifdef ASTRA_HOST_EMULATION
+    d.ptr = scratch;  // the host build's "device" memory is host memory
+#else
+    DeviceGuard g(dev);
+    if (!g.ok) return fail(ASTRA_ERR_HIP, "hipSetDevice failed");
+    int32_t *p = nullptr;
+    ASTRA_HIP_CHECK(hipGetSymbolAddress(reinterpret_cast<void **>(&p), HIP_SYMBOL(scratch)),
+                    "hipGetSymbolAddress(scratch)");
+    hipEvent_t ev = nullptr;
+    ASTRA_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreateWithFlags");
+    d.ev = ev;
+    d.ptr = p;
+#endif
+  }
+  *out = &d;
+  return ASTRA_OK;
+}
+
+// ApplyPlayerTrading for all envs of `market` (astra_high_low_trade), with the
+// checks' error word at `errors` and, when set, `ev` as the checks' event.
+int trade_impl(astra_market *market, const astra_hl_trade *t, int32_t *errors, hipEvent_t ev,
+               void *stream) {
   int32_t M = 0, L = 0, O = 0, F = 0, C = 0;
   int rc = astra_market_shape(market, &M, &L, &O, &F, &C);
   if (rc) return rc;
@@ -281,7 +330,7 @@ int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *st
                         t->market_contract_over_time, t->immediate_rewards,
                         t->rewards_since_last_action, t->fill_counts, t->best_bid_prices,
                         t->best_bid_sizes, t->best_ask_prices, t->best_ask_sizes,
-                        t->last_prices, t->errors};
+                        t->last_prices, errors};
   for (const void *p : need)
     if (M > 0 && p == nullptr)
       return fail(ASTRA_ERR_INVALID_ARGUMENT, "astra_high_low_trade: null pointer in astra_hl_trade");
@@ -306,7 +355,7 @@ int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *st
   g.bbo_out[2] = t->best_ask_prices;
   g.bbo_out[3] = t->best_ask_sizes;
   g.last_prices = t->last_prices;
-  g.errors = t->errors;
+  g.errors = errors;
   g.P = t->players;
   g.T = t->steps_per_player;
   g.S = t->max_contracts_per_trade;
@@ -323,11 +372,12 @@ int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *st
   g.abort_on_error = t->check ? 1 : 0;
   int32_t tid_before = 0, bits = 0;
   StreamMark checked;
+  checked.ev = ev;
   if (t->check) {
     if ((rc = launch_check(g, M, s))) return rc;
     if ((rc = astra_market_get_tid(market, &tid_before))) return rc;
     if (t->errors_host) {
-      ASTRA_HIP_CHECK(rt_memcpy(t->errors_host, t->errors, sizeof(int32_t), s), "error flags copy");
+      ASTRA_HIP_CHECK(rt_memcpy(t->errors_host, errors, sizeof(int32_t), s), "error flags copy");
       ASTRA_HIP_CHECK(checked.record(s), "error flags event");
     }
   }
@@ -338,7 +388,7 @@ int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *st
     ASTRA_HIP_CHECK(checked.wait(), "error flags wait");
     bits = *t->errors_host;
   } else {
-    ASTRA_HIP_CHECK(rt_memcpy(&bits, t->errors, sizeof(bits), s), "error flags copy");
+    ASTRA_HIP_CHECK(rt_memcpy(&bits, errors, sizeof(bits), s), "error flags copy");
     ASTRA_HIP_CHECK(rt_sync(s), "error flags wait");
   }
   if (bits) {
@@ -346,6 +396,34 @@ int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *st
     return fail(ASTRA_ERR_INVALID_ARGUMENT, std::string("high_low_trading.cc ") + check_text(bits));
   }
   return ASTRA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *stream) {
+  ASTRA_ABI_CHECK(t != nullptr, ==, true);
+  return trade_impl(market, t, t->errors, nullptr, stream);
+}
+
+int astra_high_low_trade_scratch(astra_market *market, const astra_hl_trade *t, void *stream) {
+  ASTRA_ABI_CHECK(market != nullptr, ==, true);
+  ASTRA_ABI_CHECK(t != nullptr, ==, true);
+  if (t->check != 1)
+    return fail(ASTRA_ERR_INVALID_ARGUMENT,
+                "astra_high_low_trade_scratch: check must be 1 (the error word is the library's "
+                "scratch, cleared by every call, so unchecked moves could not report later)");
+  if (!t->errors_host)
+    return fail(ASTRA_ERR_INVALID_ARGUMENT,
+                "astra_high_low_trade_scratch: errors_host (one int32 of pinned host memory) is "
+                "required");
+  ScratchDevice *d = nullptr;
+  int rc = scratch_device(astra_game_device(market), &d);
+  if (rc) return rc;
+  // word 0 starts at zero: a fill kernel (the last call left its bits there)
+  if ((rc = astra_fill_i32(d->ptr, 1, 0, stream))) return rc;
+  return trade_impl(market, t, d->ptr, d->ev, stream);
 }
 
 int astra_high_low_rewards(const int32_t *src, int64_t num_envs, int32_t players, int32_t player,

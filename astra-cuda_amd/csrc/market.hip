@@ -1806,9 +1806,10 @@ int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, i
   h->ws = static_cast<char *>(workspace);
   h->ws_bytes = workspace_bytes;
   h->lay = lay;
-  rc = init_book(h, as_stream(stream));
-  // zero the order records once so a fresh workspace holds no garbage
-  if (!rc) rc = launch_fill(h->ws + lay.records, (int64_t)M * O * 4, 0u, as_stream(stream), "init");
+  // the whole workspace to 0 once (order records and alignment padding included, so a
+  // fresh workspace holds no garbage), then the empty book's NULL words
+  rc = launch_fill(h->ws, (int64_t)(lay.total / 4), 0u, as_stream(stream), "init");
+  if (!rc) rc = init_book(h, as_stream(stream));
   if (rc) {
     delete h;
     return rc;

@@ -47,6 +47,7 @@ struct DeviceGuard {
 };
 inline void rt_device_sync(int) {}
 struct StreamMark {
+  hipEvent_t ev = nullptr;
   hipError_t record(hipStream_t) { return hipSuccess; }
   hipError_t wait() { return hipSuccess; }
 };
@@ -79,9 +80,12 @@ inline void rt_device_sync(int dev) {
 }
 // A point in a stream the host can wait for while later work on the stream
 // runs (one cached event per host thread and device).
+// An event recorded on a stream and waited for: `ev` if the caller set one,
+// else one created on first use per host thread and device and kept.
 struct StreamMark {
   hipEvent_t ev = nullptr;
   hipError_t record(hipStream_t st) {
+    if (ev) return hipEventRecord(ev, st);
     static thread_local hipEvent_t cache[64] = {};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);

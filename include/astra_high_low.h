@@ -78,6 +78,18 @@ typedef struct astra_hl_trade {
  * envs of `market` (N = its market count; C >= players customers). */
 int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *stream);
 
+/* No counterpart in the reference: astra_high_low_trade for callers that cannot
+ * allocate device memory (serving loops, harnesses that forbid hipMalloc). The
+ * checks' error word is the library's own per-device scratch (one static device
+ * array of 64 int32 per GPU, holding the word whatever N is) instead of
+ * t->errors, which is ignored and may be NULL. Requires check = 1 (the word is
+ * cleared by every call, so unchecked moves could not report later) and
+ * errors_host (one int32 of pinned host memory). Results and errors are those of
+ * astra_high_low_trade. Allocates nothing: the device address of the scratch and
+ * an event are set up once per device on its first call there. Calls that
+ * overlap on one GPU (other host threads or streams) share its scratch and race. */
+int astra_high_low_trade_scratch(astra_market *market, const astra_hl_trade *t, void *stream);
+
 /* FillObservationTensor(player, values) (high_low_trading.cc:510-602). */
 typedef struct astra_hl_observation {
   float *values;                  /* [N, 6 + 1 + 6P + 5] */

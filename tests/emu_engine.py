@@ -286,7 +286,7 @@ class EmuHighLow:
         """[N,P*T,3] view of the env-minor [P*T,3,N] storage."""
         return np.transpose(self._mcot, (2, 0, 1))
 
-    def trade(self, move, player, tmn, check=1):
+    def trade(self, move, player, tmn, check=1, entry="astra_high_low_trade"):
         self.move = np.ascontiguousarray(move, np.int32)
         t = self._HLTrade()
         ptr = lambda a: a.ctypes.data  # noqa: E731
@@ -307,7 +307,7 @@ class EmuHighLow:
         t.players, t.steps_per_player = self.P, self.T
         t.max_contracts_per_trade, t.max_contract_value = self.S, self.V
         t.player, t.trade_move_number, t.check = player, tmn, check
-        return lib().astra_high_low_trade(self.market.h, ctypes.byref(t), None)
+        return getattr(lib(), entry)(self.market.h, ctypes.byref(t), None)
 
     def observation(self, player, current_round):
         import math

@@ -151,3 +151,39 @@ def test_emulated_rewards_entry_point(N, P):
         assert lib().astra_high_low_rewards(src.ctypes.data, N, P, p, col.ctypes.data, None) == 0
         assert np.array_equal(col, src[:, p].astype(np.float32))
     assert lib().astra_high_low_rewards(src.ctypes.data, N, P, P, dst.ctypes.data, None) != 0
+
+
+def test_emulated_scratch_trade_entry_point():
+    """astra_high_low_trade_scratch (the allocation-free move, no counterpart in the
+    reference) on the host build: random games against the oracle through it, two
+    games in a row, the second smaller; its own error word unused; a failed check
+    returns the error and changes nothing; unchecked moves and a missing host word
+    are refused."""
+    from emu_engine import lib
+    for N, seed in ((40, 21), (9, 22)):
+        P, T, S, cM, V = 5, 4, 5, 5, 30
+        rng = np.random.default_rng(seed)
+        o = OracleHighLow(N, P, T, S, cM, V)
+        e = EmuHighLow(N, P, T, S, cM, V, (o.L, o.O, o.F, o.C))
+        e.errors = None
+        chance, moves = random_game(rng, N, P, T, S, cM, V)
+        for c in chance:
+            o.apply_action(c)
+        _setup(o, e)
+        for k, mv in enumerate(moves[:8]):
+            player = o.current_player()
+            o.apply_action(mv)
+            assert e.trade(mv, player, k, entry="astra_high_low_trade_scratch") == 0
+            _compare(o, e, f"N={N} move {k}")
+        bad = moves[8].copy()
+        bad[N // 2, 3] = S + 1
+        ws, tid = e.market.ws.copy(), e.market.global_tid
+        assert e.trade(bad, o.current_player(), 8, entry="astra_high_low_trade_scratch") != 0
+        assert "ask_sizes" in lib().astra_last_error().decode()
+        assert np.array_equal(e.market.ws, ws) and e.market.global_tid == tid
+        _compare(o, e, f"N={N} after the failed check")
+    assert e.trade(moves[8], 3, 8, check=0, entry="astra_high_low_trade_scratch") != 0
+    assert "check must be 1" in lib().astra_last_error().decode()
+    e.errors_host = None
+    assert e.trade(moves[8], 3, 8, entry="astra_high_low_trade_scratch") != 0
+    assert "errors_host" in lib().astra_last_error().decode()
