@@ -20,8 +20,10 @@ arrays wrap like torch's int32 kernels), on top of the C market oracle
 
 What pins each part (tests/test_high_low_oracle.py; values worked out on paper in
 tests/high_low_cases.py, not by running any implementation): the chance moves, the
-trading move, every reward, portfolio and market row, the returns, one observation
-and ExposeInfo by the hand-derived four-player game; the reward formula also by an
+trading move, every reward, portfolio and market row, the returns, ExposeInfo and
+four observations, one for each branch of the round selection (:559-584: round 0,
+player 0, the last player, a middle player, each shown to differ from what the
+other branches would give), by the hand-derived four-player game; the reward formula also by an
 identity (without penalties a player's rewards over a game sum to its return plus
 |target|*V for a customer); the input checks by a hand case; the text renderings by
 hand-written text; DoReset by replaying the hand game after a reset; the order

@@ -27,6 +27,13 @@
  * (src/tests/unit_tests/market_tests.cu), hand-derived traces of eviction
  * aliasing and fill overflow, conservation and uncrossed-book invariants, and
  * an independently written pure-Python simulator on small random books.
+ * om_clear_quotes: a cleared market behaves from then on like a fresh book with
+ * the same TID counter (fills, BBOs, text, portfolio deltas) through ring
+ * wrap-arounds, its heads, tails and ring position equal a fresh book's, and
+ * the markets not selected go on as without the clear. om_clone: the copy
+ * evolves exactly like its source, every state array equal after every step,
+ * and independently of it. Each check is shown to catch planted mistakes
+ * (tests/test_oracle_clear_clone.py). No function here is left unpinned.
  */
 #include "market_oracle.h"
 

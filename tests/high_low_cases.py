@@ -43,6 +43,32 @@ HAND_GAME = {
     "obs": [0, 1, 0, float(np.float32(np.sin(np.pi))), -1, 1, 0.5,
             1, 30, 1, 1, -1, 18, 1, 30, 1, 1, 0, 7, 10, 30, 0, 0, 0, 0, 26, 24, 2, 1, 1, -25,
             18, 30, 2, 1, 25],
+    # The other round selections of :559-584. Each move writes its quote into the
+    # acting player's row of the current round and every player's contracts and
+    # cash after the move into all rows of that round (:290-291); rows of a round
+    # not reached yet are zeros. Positions (contracts, cash): all (0, 0) after
+    # move 0; after moves 1-2 p0 (-1, 18), p1 (1, -18); after moves 3-7 p0 (-1, 18),
+    # p1 (0, 7), p2 (0, 0), p3 (1, -25). The last five words are the BBO and last
+    # price after the move (bid px, ask px, bid sz, ask sz, last); sin and cos of
+    # 2*pi*player/P are computed in double and stored as float32 (:532-534).
+    "more_obs": [
+        # round 0 (current_round == 0): player 1 after move 1 sees round 0 so far
+        # (players 2 and 3 have not quoted yet); a value cheater with candidate 20
+        (1, 1, [1, 0, 0, float(np.float32(np.sin(np.pi / 2))), float(np.float32(np.cos(np.pi / 2))),
+                20, 0.0,
+                12, 18, 2, 1, -1, 18, 18, 25, 3, 1, 1, -18, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0,
+                18, 25, 2, 1, 18]),
+        # player 0 in round 1 (after move 5) sees all of round 0
+        (5, 0, [1, 0, 0, 0.0, 1.0, 10, 0.5,
+                12, 18, 2, 1, -1, 18, 18, 25, 3, 1, 0, 7, 10, 30, 0, 0, 0, 0, 26, 24, 2, 1, 1, -25,
+                18, 30, 2, 1, 25]),
+        # the last player (3) in round 1 (after move 6) sees round 1 so far: its own
+        # quote not yet written, its position already; a customer with target 2
+        (6, 3, [0, 0, 1, float(np.float32(np.sin(3 * np.pi / 2))),
+                float(np.float32(np.cos(3 * np.pi / 2))), 2, 0.5,
+                1, 30, 1, 1, -1, 18, 1, 30, 1, 1, 0, 7, 1, 30, 1, 1, 0, 0, 0, 0, 0, 0, 1, -25,
+                18, 30, 2, 1, 25]),
+    ],
 }
 
 

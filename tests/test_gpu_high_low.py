@@ -125,6 +125,10 @@ def test_gpu_hand_game():
         if k == HAND_GAME["obs_after"]:
             s.fill_observation_tensor(HAND_GAME["obs_player"], values)
             assert values[0].tolist() == HAND_GAME["obs"]
+        for after, player, want in HAND_GAME["more_obs"]:
+            if k == after:
+                s.fill_observation_tensor(player, values)
+                assert values[0].tolist() == want, (after, player)
     ret = torch.zeros((1, 4), dtype=torch.float32, device=DEV)
     s.fill_returns(ret)
     assert ret[0].tolist() == HAND_GAME["returns"]

@@ -100,6 +100,9 @@ def test_emulated_hand_game():
         assert e.market_contract_over_time[0, k].tolist() == HAND_GAME["market_rows"][k]
         if k == HAND_GAME["obs_after"]:
             assert e.observation(HAND_GAME["obs_player"], 1)[0].tolist() == HAND_GAME["obs"]
+        for after, player, want in HAND_GAME["more_obs"]:
+            if k == after:  # current round after move k of 4 players: (k + 1) // 4
+                assert e.observation(player, (k + 1) // 4)[0].tolist() == want, (after, player)
 
 
 @pytest.mark.parametrize("host_word", [True, False], ids=["errors_host", "no_errors_host"])

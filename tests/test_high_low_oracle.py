@@ -17,6 +17,9 @@ def _play_hand(o):
                     o.market.customer_portfolios[0].tolist(), o.market_contract_over_time[0, k].tolist()))
         if k == HAND_GAME["obs_after"]:
             obs = o.fill_observation_tensor(HAND_GAME["obs_player"])[0].tolist()
+        for after, player, want in HAND_GAME["more_obs"]:
+            if k == after:
+                assert o.fill_observation_tensor(player)[0].tolist() == want, (after, player)
     return out, obs
 
 
@@ -122,3 +125,42 @@ def test_game_keeps_the_reference_market_caps():
     if torch.cuda.device_count() == 0:
         with pytest.raises(RuntimeError, match="device_id < device_count"):
             astra.load_game("high_low_trading", dict(prm, market_extended_shapes=True)).new_initial_state()
+
+
+def test_observation_cases_tell_the_round_selections_apart():
+    """The hand observations pin the round selection (:559-584): for each case,
+    every other plausible choice of rounds (the current round for all players,
+    the previous one for all, or the wrap-around split at the observing player;
+    a round index of -1 reads the last round, as torch's negative indexing would)
+    that differs from the reference's choice gives a vector other than the hand
+    one. (For player 0 the wrap-around split is the previous round for all: the
+    same choice as its own branch.)"""
+    o = OracleHighLow(**{k: v for k, v in HAND_GAME["params"].items()})
+    for c in HAND_GAME["chance"]:
+        o.apply_action(c)
+    cases = HAND_GAME["more_obs"] + [(HAND_GAME["obs_after"], HAND_GAME["obs_player"], HAND_GAME["obs"])]
+    P = o.P
+    checked = 0
+    for k, mv in enumerate(HAND_GAME["moves"]):
+        o.apply_action(np.array([mv], np.int32))
+        for after, player, want in cases:
+            if k != after:
+                continue
+            cr = (o.move_number - 4) // P
+            if cr == 0 or player == P - 1:
+                ref = [cr] * P
+            elif player == 0:
+                ref = [cr - 1] * P
+            else:
+                ref = [cr if p < player else cr - 1 for p in range(P)]
+            pcot = o.player_contract_over_time[0]
+            base = o.fill_observation_tensor(player)[0]
+            assert base.tolist() == want
+            for rounds in ([cr] * P, [cr - 1] * P, [cr if p < player else cr - 1 for p in range(P)]):
+                if rounds == ref:
+                    continue
+                v = base.copy()
+                v[7:7 + 6 * P] = np.concatenate([pcot[p, rounds[p]] for p in range(P)]).astype(np.float32)
+                assert v.tolist() != want, (after, player, rounds)
+                checked += 1
+    assert checked >= 5
