@@ -23,7 +23,9 @@ from dataclasses import dataclass
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "libmarket_oracle.so")
+# ASTRA_ORACLE_LIB: another build of the same source (the Makefile's `sanitize`
+# target) for a sanitizer run of the test suite
+_LIB_PATH = os.environ.get("ASTRA_ORACLE_LIB") or os.path.join(_HERE, "libmarket_oracle.so")
 
 _i32p = ctypes.POINTER(ctypes.c_int32)
 _u8p = ctypes.POINTER(ctypes.c_uint8)

@@ -28,6 +28,27 @@ DEPS = SRCS + [os.path.join(CSRC, "runtime.h"), os.path.join(CSRC, "game_move.h"
 _lib = None
 
 
+# ASTRA_EMU_SANITIZE=1 builds (and loads) the library with AddressSanitizer and
+# UndefinedBehaviorSanitizer on the host code; the Python process must then run
+# with the sanitizer runtime preloaded (see sanitize_env()).
+SANITIZE = os.environ.get("ASTRA_EMU_SANITIZE", "") not in ("", "0")
+if SANITIZE:
+    EMU_LIB = os.path.join(BUILD_DIR, "libastra_market_emu_asan.so")
+SAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+             "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer"]
+
+
+def sanitize_env() -> dict:
+    """Environment for a process that loads the sanitized build: the clang
+    AddressSanitizer runtime preloaded (it carries the UBSan handlers too)."""
+    from astra_cuda.build import hipcc
+    clang = os.path.join(os.path.dirname(os.path.realpath(hipcc())), "..", "llvm", "bin", "clang")
+    rt = subprocess.run([clang, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True,
+                        text=True, check=True).stdout.strip()
+    return {"LD_PRELOAD": rt, "ASAN_OPTIONS": "detect_leaks=0:abort_on_error=1",
+            "UBSAN_OPTIONS": "print_stacktrace=1:halt_on_error=1", "ASTRA_EMU_SANITIZE": "1"}
+
+
 def build(force: bool = False) -> str:
     if not force and os.path.exists(EMU_LIB) and \
             os.path.getmtime(EMU_LIB) >= max(os.path.getmtime(d) for d in DEPS):
@@ -35,7 +56,8 @@ def build(force: bool = False) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     from astra_cuda.build import hipcc
     tmp = f"{EMU_LIB}.{os.getpid()}.tmp"
-    cmd = [hipcc(), "-DASTRA_HOST_EMULATION", "--cuda-host-only", "-O2", "-g", "-std=c++17",
+    opt = ["-O1", *SAN_FLAGS] if SANITIZE else ["-O2"]
+    cmd = [hipcc(), "-DASTRA_HOST_EMULATION", "--cuda-host-only", *opt, "-g", "-std=c++17",
            "-fPIC", "-shared", f"-I{os.path.join(ROOT, 'include')}", *SRCS, "-o", tmp]
     subprocess.run(cmd, check=True, capture_output=True)
     os.replace(tmp, EMU_LIB)  # atomic: parallel test workers each build their own copy
