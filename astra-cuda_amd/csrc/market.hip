@@ -55,6 +55,10 @@ using namespace astra_rt;
 namespace {
 
 constexpr uint32_t kNull16 = 0xFFFFu;
+// Bit 15 of a head slot in the tob word: that head order's size is in the
+// workspace's head-size cache (slots are below 0x8000 since O <= 32768; NULL is
+// 0xFFFF and carries no flag).
+constexpr uint32_t kSizeKnown = 0x8000u;
 constexpr int kFillThreads = 256;
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -71,7 +75,7 @@ inline int mask_words_for(int32_t L) {
 // Byte offsets of the book arrays inside the workspace.
 struct Layout {
   int W;
-  size_t masks, next_slot, bbo, tob, levels, records, portfolios, total;
+  size_t masks, next_slot, bbo, tob, hsz, levels, records, portfolios, total;
 };
 
 Layout make_layout(int64_t M, int64_t L, int64_t O, int64_t C) {
@@ -86,6 +90,8 @@ Layout make_layout(int64_t M, int64_t L, int64_t O, int64_t C) {
   off = align_up(off + (size_t)2 * M * 4, 256);
   l.tob = off;
   off = align_up(off + (size_t)M * 4, 256);
+  l.hsz = off;
+  off = align_up(off + (size_t)2 * M * 4, 256);
   l.levels = off;
   off = align_up(off + (size_t)M * L * 8, 256);
   l.records = off;
@@ -120,7 +126,9 @@ struct Book {
   uint64_t *masks;            // [2][W][M]: side 0 = bid, 1 = ask
   int32_t *next_slot;         // [M], in [0, O)
   int32_t *bbo;               // [2][M]: best bid price, best ask price (NULL: empty side)
-  uint32_t *tob;              // [M]: head slots of the best levels, bid | ask << 16
+  uint32_t *tob;              // [M]: head slots of the best levels, bid | ask << 16, each
+                              // with kSizeKnown set when its size is in hsz
+  int32_t *hsz;               // [2][M]: sizes of those head orders (valid where flagged)
   uint16_t *levels;           // [M][L][4] = {bid_head, bid_tail, ask_head, ask_tail}
   uint4 *records;             // [M][O] = {size, customer, tid, price | next << 16}
   int32_t *portfolios;        // [M][C][2] = {contracts, cash}
@@ -134,6 +142,7 @@ Book book_of(const astra_market *h) {
   b.next_slot = reinterpret_cast<int32_t *>(h->ws + h->lay.next_slot);
   b.bbo = reinterpret_cast<int32_t *>(h->ws + h->lay.bbo);
   b.tob = reinterpret_cast<uint32_t *>(h->ws + h->lay.tob);
+  b.hsz = reinterpret_cast<int32_t *>(h->ws + h->lay.hsz);
   b.levels = reinterpret_cast<uint16_t *>(h->ws + h->lay.levels);
   b.records = reinterpret_cast<uint4 *>(h->ws + h->lay.records);
   b.portfolios = reinterpret_cast<int32_t *>(h->ws + h->lay.portfolios);
@@ -482,6 +491,7 @@ struct MarketCtx {
   int32_t *pf;
   int32_t ns;             // ring position after the inserts
   bool bid_ok, ask_ok;
+  bool keep_b, keep_a;    // a head the call left untouched whose size the cache holds
   GameQuote gq;           // the game's move (GAME only)
   bool abort;             // GAME: a failed check stops the whole move
 };
@@ -737,7 +747,9 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   const int bb = bid_top ? bid_px : bb0;
   const int ba = ask_top ? ask_px : ba0;
   const bool cross = bb >= 0 && ba < L && bb >= ba;
-  const uint32_t hb0 = tob & kNull16, ha0 = tob >> 16;
+  const uint32_t hb0f = tob & kNull16, ha0f = tob >> 16;  // with their size flags
+  const uint32_t hb0 = hb0f == kNull16 ? kNull16 : (hb0f & ~kSizeKnown);
+  const uint32_t ha0 = ha0f == kNull16 ? kNull16 : (ha0f & ~kSizeKnown);
 
   // ---- round trip 2 ----
   // The insert levels' words: unconditional loads (level 0 stands in for a
@@ -839,7 +851,17 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
     s.ah = ask_top ? aslot : ha0;
     s.arec = patched(s.ah, hra);
   }
-  s.have_b = s.have_a = true;
+  // The head records in registers: read above (a crossing book, or where the
+  // call hands out the BBO itself, or carried), or written by this call's
+  // inserts. A head the call does not touch and whose record it did not read
+  // keeps the size cached by an earlier call, if that call cached it.
+  const bool sizes_in = head_recs || (kSizes && carried);
+  s.have_b = bb >= 0 && (sizes_in || s.bh == bslot || s.bh == aslot);
+  s.have_a = ba < L && (sizes_in || s.ah == bslot || s.ah == aslot);
+  c.keep_b = !cross && !s.have_b && bb >= 0 && !bid_top && hb0f != kNull16 && (hb0f & kSizeKnown) &&
+             hb0 != 0x7FFFu;
+  c.keep_a = !cross && !s.have_a && ba < L && !ask_top && ha0f != kNull16 && (ha0f & kSizeKnown) &&
+             ha0 != 0x7FFFu;
   // the next levels read ahead, as the inserts left their heads
   if (bid_ok && pb == bid_px && (bword >> 16) == kNull16) pbh = bslot;
   if (ask_ok && pa == ask_px && (aword >> 16) == kNull16) pah = aslot;
@@ -1117,13 +1139,25 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
     b.next_slot[m] = c.ns;
   }
   sink.flush(out, c.pf, c.C);  // overlaps the loads above
-  const int32_t obp = (s.bb >= 0 && s.bh < (uint32_t)O) ? s.bb : ASTRA_NULL_INDEX;
-  const int32_t oap = (s.ba < L && s.ah < (uint32_t)O) ? s.ba : ASTRA_NULL_INDEX;
-  const uint32_t tob = ((s.bb >= 0 ? s.bh : kNull16) & kNull16) | ((s.ba < L ? s.ah : kNull16) << 16);
+  const bool bv = s.bb >= 0 && s.bh < (uint32_t)O, av = s.ba < L && s.ah < (uint32_t)O;
+  const int32_t obp = bv ? s.bb : ASTRA_NULL_INDEX;
+  const int32_t oap = av ? s.ba : ASTRA_NULL_INDEX;
+  // Head sizes the call knows (the record is in registers, or the call hands
+  // out the BBO and loaded it) go to the size cache; a head the call left
+  // untouched keeps the size an earlier call cached. get_bbos reads the book
+  // only for the others.
+  // (slot 0x7FFF, possible at O = 32768, is never flagged: flagged it would read
+  // as NULL)
+  const bool wb = bv && (kSizes || s.have_b) && s.bh != 0x7FFFu;
+  const bool wa = av && (kSizes || s.have_a) && s.ah != 0x7FFFu;
+  const uint32_t tob = (bv ? (s.bh | ((wb || c.keep_b) ? kSizeKnown : 0u)) : kNull16) |
+                       ((av ? (s.ah | ((wa || c.keep_a) ? kSizeKnown : 0u)) : kNull16) << 16);
   if (store) {
     b.bbo[m] = obp;
     b.bbo[M + m] = oap;
     b.tob[m] = tob;
+    if (wb) b.hsz[m] = kSizes ? obs : (int32_t)s.brec.x;
+    if (wa) b.hsz[M + m] = kSizes ? oas : (int32_t)s.arec.x;
   }
   if (MULTI && Carry<W>::kState && cy) {
 #pragma unroll
@@ -1167,18 +1201,21 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
 
 // GetBBOs (market.cu:573-597) reads the cache the last call left: the best
 // level and the size of its head order per side, (NULL, 0) for an empty side.
+// Sizes come from the head-size cache where the tob word flags them, else from
+// the head order's record in the book.
 ASTRA_HD void bbo_copy_market(const Book &b, int32_t *bid_px, int32_t *bid_sz, int32_t *ask_px,
                               int32_t *ask_sz, int64_t m) {
   const int64_t M = b.M;
   const int32_t bp = b.bbo[m], ap = b.bbo[M + m];
-  const uint32_t t = b.tob[m], bh = t & kNull16, ah = t >> 16;
+  const uint32_t t = b.tob[m], bf = t & kNull16, af = t >> 16;
+  const int32_t cb = b.hsz[m], ca = b.hsz[M + m];
+  const uint32_t bh = bf & ~kSizeKnown, ah = af & ~kSizeKnown;
+  const bool bv = bp != ASTRA_NULL_INDEX && bf != kNull16 && bh < (uint32_t)b.O;
+  const bool av = ap != ASTRA_NULL_INDEX && af != kNull16 && ah < (uint32_t)b.O;
   const uint4 *rec = b.records + m * (int64_t)b.O;
-  // Both head sizes in one round trip: unconditional loads (slot 0 stands in
-  // for a NULL head), issued before any store.
-  const bool bv = bp != ASTRA_NULL_INDEX && bh < (uint32_t)b.O;
-  const bool av = ap != ASTRA_NULL_INDEX && ah < (uint32_t)b.O;
-  const int32_t bs = reinterpret_cast<const int32_t *>(rec + (bv ? bh : 0u))[0];
-  const int32_t as = reinterpret_cast<const int32_t *>(rec + (av ? ah : 0u))[0];
+  int32_t bs = cb, as = ca;
+  if (bv && !(bf & kSizeKnown)) bs = reinterpret_cast<const int32_t *>(rec + bh)[0];
+  if (av && !(af & kSizeKnown)) as = reinterpret_cast<const int32_t *>(rec + ah)[0];
   bid_px[m] = bp;
   ask_px[m] = ap;
   bid_sz[m] = bv ? bs : 0;

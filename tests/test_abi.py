@@ -94,3 +94,13 @@ def test_no_device_fails_loudly():
     from astra_cuda import order_matching as aom
     with pytest.raises(RuntimeError, match="Astra Fatal Error"):
         aom.VecMarket(4, 128, 16, 16)
+
+
+@pytest.mark.parametrize("shape", [(10, 128, 1024, 512, 16), (7, 70, 5, 3, 4), (3, 1024, 32768, 8, 65536),
+                                   (0, 8, 1, 1, 1)])
+def test_test_side_workspace_layout_matches_the_engine(shape):
+    """tests/ws_layout.py (used to compare workspaces) describes the engine's layout."""
+    from ws_layout import layout
+    M, L, O, F, C = shape
+    rc, n, _ = _ws(*shape, flags=1)
+    assert rc == 0 and layout(M, L, O, C)["total"][1] == n
