@@ -178,36 +178,72 @@ ASTRA_HD void observation_column(const astra_hl_observation &o, int64_t n, int32
 // BBO arrays), so a wavefront loads each column of its 64 envs with one
 // coalesced load, all columns before any wait (the per-element kernel above
 // branches on the column and waits once per branch); it transposes the values in
-// LDS and stores its 64 rows, which are contiguous in `values`, a row per store.
+// LDS. Its 64 rows are one contiguous block of 64 * D floats in `values`, which
+// the wavefront writes as a flat array: 16 bytes per lane and store (`vec`: the
+// block is 16-byte aligned, since n0 * D * 4 is a multiple of 256 and `values`
+// is 16-byte aligned), else 4 bytes per lane; every store covers 1 KB (or
+// 256 B) of consecutive addresses.
 constexpr int kObsTileWaves = 2;     // wavefronts per block
-constexpr int kObsMaxColumns = 64;
 
+template <int PP>
 __global__ __launch_bounds__(kObsTileWaves * 64) void observation_tile_kernel(astra_hl_observation o,
-                                                                             int64_t N) {
+                                                                             int64_t N, int32_t vec) {
+  constexpr int32_t D = 12 + 6 * PP;  // row length; the player count is a template argument
+  constexpr int32_t pitch = D + 1;    // odd (D is even): lanes' rows fall in different banks
   extern __shared__ float obs_tile[];  // per wavefront: 64 rows of `pitch` floats
   const int lane = (int)(threadIdx.x % 64), w = (int)(threadIdx.x / 64);
   const int64_t n0 = ((int64_t)blockIdx.x * kObsTileWaves + w) * 64;
-  const int32_t P = o.players, player = o.player, D = 12 + 6 * P;
-  const int32_t pitch = D + 1;  // odd (D is even): lanes' rows fall in different banks
+  const int32_t player = o.player;
   const int64_t n = n0 + lane < N ? n0 + lane : N - 1;  // clamped: no branch around a load
-  const int32_t perm = o.player_permutation[n * P + player];
+  // the env's own words (role, private information), then one coalesced load per
+  // column of the rounds and the BBO, all issued before any wait
+  const int32_t perm = o.player_permutation[n * PP + player];
   const int32_t cv0 = o.contract_values[n * 3], cv1 = o.contract_values[n * 3 + 1];
   const uint8_t settle = o.contract_high_settle[n];
-  const int32_t target = o.target_positions[n * P + player];
-  int32_t word[kObsMaxColumns];
+  const int32_t target = o.target_positions[n * PP + player];
+  int32_t word[D];
 #pragma unroll
-  for (int32_t j = 0; j < kObsMaxColumns; ++j) {  // columns past the row reload the last one
-    const ObsColumn c = obs_column(o, j < D ? j : D - 1);
+  for (int32_t j = 7; j < D; ++j) {
+    const ObsColumn c = obs_column(o, j);
     word[j] = c.src[n * c.stride];
   }
   float *tile = obs_tile + w * 64 * pitch;
 #pragma unroll
-  for (int32_t j = 0; j < kObsMaxColumns; ++j)
-    if (j < D)
-      tile[lane * pitch + j] = obs_value(obs_column(o, j), j, perm, word[j], cv0, cv1, settle, target);
+  for (int32_t j = 0; j < D; ++j)
+    tile[lane * pitch + j] =
+        obs_value(obs_column(o, j), j, perm, j < 7 ? perm : word[j], cv0, cv1, settle, target);
   __syncthreads();
-  if (lane < D)
-    for (int32_t e = 0; e < 64 && n0 + e < N; ++e) o.values[(n0 + e) * D + lane] = tile[e * pitch + lane];
+  const int64_t rows = N - n0 < 64 ? N - n0 : 64;
+  if (rows <= 0) return;
+  const int32_t total = (int32_t)rows * D;  // floats of this wavefront's rows
+  float *dst = o.values + n0 * D;
+  // flat index f of the block is row f / D, column f % D of the tile
+  if (vec && rows == 64) {
+    for (int32_t f = lane * 4; f < total; f += 256) {
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int32_t e = (f + q) / D, jj = (f + q) - e * D;
+        v[q] = tile[e * pitch + jj];
+      }
+      *reinterpret_cast<float4 *>(dst + f) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  } else {
+    for (int32_t f = lane; f < total; f += 64) {
+      const int32_t e = f / D, jj = f - e * D;
+      dst[f] = tile[e * pitch + jj];
+    }
+  }
+}
+
+template <int PP>
+void launch_observation_tile(const astra_hl_observation &o, hipStream_t s) {
+  const int64_t per_block = 64 * kObsTileWaves;
+  const unsigned blocks = (unsigned)(((int64_t)o.num_envs + per_block - 1) / per_block);
+  const size_t lds = (size_t)per_block * (13 + 6 * PP) * sizeof(float);
+  const int32_t vec = reinterpret_cast<uintptr_t>(o.values) % 16 == 0 ? 1 : 0;
+  hipLaunchKernelGGL(observation_tile_kernel<PP>, dim3(blocks), dim3(per_block), lds, s, o,
+                     (int64_t)o.num_envs, vec);
 }
 
 // The rewards as float32: column `col` of the [n, stride] int32 array (col >= 0),
@@ -479,11 +515,16 @@ int astra_high_low_observation(const astra_hl_observation *o, void *stream) {
   return ASTRA_OK;
 #else
   if (rows) {
-    const int64_t per_block = 64 * kObsTileWaves;
-    const unsigned blocks = (unsigned)(((int64_t)o->num_envs + per_block - 1) / per_block);
-    const size_t lds = (size_t)per_block * (13 + 6 * o->players) * sizeof(float);
-    hipLaunchKernelGGL(observation_tile_kernel, dim3(blocks), dim3(per_block), lds,
-                       as_stream(stream), *o, (int64_t)o->num_envs);
+    switch (o->players) {
+      case 1: launch_observation_tile<1>(*o, as_stream(stream)); break;
+      case 2: launch_observation_tile<2>(*o, as_stream(stream)); break;
+      case 3: launch_observation_tile<3>(*o, as_stream(stream)); break;
+      case 4: launch_observation_tile<4>(*o, as_stream(stream)); break;
+      case 5: launch_observation_tile<5>(*o, as_stream(stream)); break;
+      case 6: launch_observation_tile<6>(*o, as_stream(stream)); break;
+      case 7: launch_observation_tile<7>(*o, as_stream(stream)); break;
+      default: launch_observation_tile<8>(*o, as_stream(stream)); break;
+    }
   } else {
     hipLaunchKernelGGL(observation_kernel, dim3(grid_for(total)), dim3(kBlock), 0,
                        as_stream(stream), *o, total);
