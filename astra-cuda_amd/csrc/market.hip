@@ -949,11 +949,23 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
     // Records of heads that changed (the entry heads come from the prologue);
     // every size change is written through, so memory is current.
     if constexpr (BookMem::kStaged) {
-      // On the staged book a read costs no memory traffic, so both head
-      // records and, when not read ahead yet, the next level's head of each
-      // side are read every pass, all issued before the first wait (the
-      // conditional reads below would each wait on their own).
-      if (!s.ahead) {
+      // On the staged book a read costs instructions, not memory traffic: both
+      // head records are read every pass, issued before one wait, and an
+      // emptied level's successor is looked up when it empties (below), so the
+      // read-ahead bookkeeping of the global-memory loop drops out.
+      s.brec = bk.record(s.bh);
+      s.arec = bk.record(s.ah);
+      s.have_b = s.have_a = true;
+    } else {
+      if (!s.have_b) {
+        s.brec = bk.record(s.bh);
+        s.have_b = true;
+      }
+      if (!s.have_a) {
+        s.arec = bk.record(s.ah);
+        s.have_a = true;
+      }
+      if (!s.ahead) {  // read the next level of each side ahead
         uint64_t t[W];
 #pragma unroll
         for (int i = 0; i < W; ++i) t[i] = s.bm[i];
@@ -963,42 +975,12 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
         for (int i = 0; i < W; ++i) t[i] = s.am[i];
         mask_clear<W>(t, s.ba);
         s.pa = mask_lowest<W>(t, L);
-      }
-      const uint4 br = bk.record(s.bh), ar = bk.record(s.ah);
-      const uint32_t pbh = bk.head(s.pb >= 0 ? s.pb : 0, 0);
-      const uint32_t pah = bk.head(s.pa < L ? s.pa : 0, 1);
-      s.brec = br;
-      s.arec = ar;
-      s.have_b = s.have_a = true;
-      if (!s.ahead) {
-        s.pbh = pbh;
-        s.pah = pah;
+        // both heads in one round trip: unconditional loads (level 0 stands in
+        // for a side with no next level), nothing waits on them in this block
+        s.pbh = bk.head(s.pb >= 0 ? s.pb : 0, 0);
+        s.pah = bk.head(s.pa < L ? s.pa : 0, 1);
         s.ahead = true;
       }
-    }
-    if (!s.have_b) {
-      s.brec = bk.record(s.bh);
-      s.have_b = true;
-    }
-    if (!s.have_a) {
-      s.arec = bk.record(s.ah);
-      s.have_a = true;
-    }
-    if (!s.ahead) {  // read the next level of each side ahead
-      uint64_t t[W];
-#pragma unroll
-      for (int i = 0; i < W; ++i) t[i] = s.bm[i];
-      mask_clear<W>(t, s.bb);
-      s.pb = mask_highest<W>(t);
-#pragma unroll
-      for (int i = 0; i < W; ++i) t[i] = s.am[i];
-      mask_clear<W>(t, s.ba);
-      s.pa = mask_lowest<W>(t, L);
-      // both heads in one round trip: unconditional loads (level 0 stands in
-      // for a side with no next level), nothing waits on them in this block
-      s.pbh = bk.head(s.pb >= 0 ? s.pb : 0, 0);
-      s.pah = bk.head(s.pa < L ? s.pa : 0, 1);
-      s.ahead = true;
     }
     // On the staged book a pass costs instructions, not memory round trips,
     // so the short zero-size walk pays there (in global memory it does not).
@@ -1061,11 +1043,16 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
         bk.set_word(s.bb, 0, 0xFFFFFFFFu);
         mask_clear<W>(s.bm, s.bb);
         if (STATS) ++s.emptied;
-        // the next level is the one read ahead at the top of this pass (pb is
-        // the highest level below bb in the same mask, and only this pop has
-        // changed the mask since)
-        s.bb = s.pb;
-        s.bh = s.bb >= 0 ? (s.pbh & kNull16) : kNull16;
+        if constexpr (BookMem::kStaged) {  // the highest remaining level and its head
+          s.bb = mask_highest<W>(s.bm);
+          s.bh = s.bb >= 0 ? bk.head(s.bb, 0) : kNull16;
+        } else {
+          // the next level is the one read ahead at the top of this pass (pb
+          // is the highest level below bb in the same mask, and only this pop
+          // has changed the mask since)
+          s.bb = s.pb;
+          s.bh = s.bb >= 0 ? (s.pbh & kNull16) : kNull16;
+        }
         s.have_b = false;
         s.ahead = false;
       } else if (nh != s.bh) {
@@ -1080,8 +1067,13 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
         bk.set_word(s.ba, 1, 0xFFFFFFFFu);
         mask_clear<W>(s.am, s.ba);
         if (STATS) ++s.emptied;
-        s.ba = s.pa;
-        s.ah = s.ba < L ? (s.pah & kNull16) : kNull16;
+        if constexpr (BookMem::kStaged) {  // the lowest remaining level and its head
+          s.ba = mask_lowest<W>(s.am, L);
+          s.ah = s.ba < L ? bk.head(s.ba, 1) : kNull16;
+        } else {
+          s.ba = s.pa;
+          s.ah = s.ba < L ? (s.pah & kNull16) : kNull16;
+        }
         s.have_a = false;
         s.ahead = false;
       } else if (nh != s.ah) {
