@@ -610,21 +610,19 @@ def game_cpu_baseline(args, cfg, chance, host_moves, N, T0, K):
             "host_cpu": model, "host_cpus_available": avail}
 
 
-def profile_traffic(profile: str, kernel: str, window):
+def profile_traffic(prefix: str, kernel: str, window):
     """HBM bytes per launch of `kernel` over the launches of steps [window) from a
-    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/
-    (copy-calibrated), or (None, None) when the summary holds no figure for
-    exactly that window (traffic depends on the book's state, so a figure from
-    other steps would describe other work)."""
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/ whose name
+    starts with `prefix` (copy-calibrated), or (None, None) when no summary holds a
+    figure for exactly that window (traffic depends on the book's state, so a
+    figure from other steps would describe other work)."""
+    import glob
     key = f"traffic_bytes_per_launch[void {kernel}][{window[0]},{window[1]}]:"
-    path = os.path.join(ROOT, "profiles", profile)
-    try:
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", prefix + "*.md"))):
         with open(path) as f:
             for line in f:
                 if line.startswith(key):
                     return float(line.split(":", 1)[1]), os.path.relpath(path, ROOT)
-    except OSError:
-        pass
     return None, None
 
 
@@ -636,7 +634,7 @@ def measured_traffic(cfg, M, bbo, window):
     words = 1
     while words * 64 < cfg.L:
         words *= 2
-    return profile_traffic(f"quote_match_config{cfg.index}_{cfg.name}_hbm_traffic.md",
+    return profile_traffic(f"quote_match_config{cfg.index}_{cfg.name}_",
                            f"quote_match_kernel<{words}, false, false, false, false>", window)
 
 
@@ -645,7 +643,7 @@ def game_traffic(cfg, N, window):
     profile_traffic)."""
     if N != cfg.envs:
         return None, None
-    return profile_traffic(f"game_move_config5_{cfg.name}_kernel_trace.md",
+    return profile_traffic(f"game_move_config5_{cfg.name}_",
                            "quote_match_kernel<2, false, true, false, true>", window)
 
 

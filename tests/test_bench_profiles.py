@@ -31,8 +31,11 @@ def test_driver_window_is_the_end_of_the_run():
 def test_matching_kernel_traffic_is_found_for_config3_driver_window():
     cfg = CONFIGS[3]
     traffic, src = bench.measured_traffic(cfg, cfg.M, cfg.bbo_every_step, _window(cfg.steps))
-    assert src == "profiles/quote_match_config3_stress_100k_hbm_traffic.md"
+    assert src.startswith("profiles/quote_match_config3_stress_100k_"), src
     assert traffic is not None and traffic > 0
+    # every summary that holds a figure for this window holds the same one
+    with open(os.path.join(ROOT, "profiles", "quote_match_config3_stress_100k_hbm_traffic.md")) as f:
+        assert f"]: {int(traffic)}" in f.read()
 
 
 def test_game_move_traffic_is_found_for_config5_driver_window():
@@ -48,3 +51,11 @@ def test_other_workloads_and_windows_report_no_traffic():
     assert bench.measured_traffic(cfg, cfg.M // 2, cfg.bbo_every_step, w) == (None, None)
     assert bench.measured_traffic(cfg, cfg.M, cfg.bbo_every_step, (5, 25)) == (None, None)
     assert bench.game_traffic(GAME_CONFIG, GAME_CONFIG.envs + 1, w) == (None, None)
+
+
+def test_matching_kernel_traffic_is_found_for_configs_2_and_4_driver_windows():
+    for idx, name in ((2, "readme_shape"), (4, "deep_book")):
+        cfg = CONFIGS[idx]
+        traffic, src = bench.measured_traffic(cfg, cfg.M, cfg.bbo_every_step, _window(cfg.steps))
+        assert src == f"profiles/quote_match_config{idx}_{name}_window.md", src
+        assert traffic is not None and traffic > 0
