@@ -217,6 +217,22 @@ ASTRA_HD int ctz64(uint64_t x) {  // x != 0
 #endif
 }
 
+// A market still crossing when at most this many lanes of its wavefront are
+// still in their matching loop, and about to walk zero-size orders, is staged
+// at once rather than after the pass budget. Not in the game move: at the
+// config-5 shape (10,000 envs, 32 per wavefront) it made the move 16% slower.
+constexpr int32_t kEarlyStageLanes = 2;
+
+// How many lanes of the wavefront execute this point together (the host build
+// runs one market at a time: 1).
+ASTRA_HD int32_t lanes_here() {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return (int32_t)__popcll(__ballot(1));
+#else
+  return 1;
+#endif
+}
+
 // Fire-and-forget add with int32 wrap-around.
 ASTRA_HD void add_i32(int32_t *p, int32_t v) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -929,8 +945,10 @@ ASTRA_HD bool zero_walk(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, 
 }
 
 // match_orders_kernel's crossing loop (market.cu:145-274). Runs at most
-// `budget` passes and stops early when the sink is full; returns false (state
-// intact, nothing of the next pass done) when it stopped before the end.
+// `budget` passes and stops early when the sink is full, or (EARLY, in global
+// memory) before a zero-size walk of a lane left nearly alone
+// (kEarlyStageLanes); returns false (state intact, nothing of the next pass
+// done) when it stopped before the end.
 //
 // Two loop states repeat forever (both arise from ring-slot reuse): a size-0
 // head that links to itself (each pass emits the same zero-size fill and
@@ -938,7 +956,7 @@ ASTRA_HD bool zero_walk(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, 
 // s and -s alternate). The reference loops until F fills and then writes -1;
 // here the owed rows are handed to the caller in `bulk`, the final state is set
 // directly, and the count is -1, which is the same result.
-template <int W, bool STATS, class BookMem, class Sink>
+template <int W, bool STATS, bool EARLY, class BookMem, class Sink>
 ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, Sink &sink,
                          const FillOut &out, Bulk &bulk, int32_t budget) {
   const int32_t L = c.L, O = c.O, F = c.F;
@@ -980,6 +998,20 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
         s.pbh = bk.head(s.pb >= 0 ? s.pb : 0, 0);
         s.pah = bk.head(s.pa < L ? s.pa : 0, 1);
         s.ahead = true;
+      }
+      // A lane that is one of at most kEarlyStageLanes still looping in its
+      // wavefront and is about to walk a run of zero-size orders stops here
+      // when staging is enabled: each further pass would cost the wavefront a
+      // memory round trip (3-4 us under load), while the staged book walks
+      // such a run at instruction speed (0.2 us a row). Lanes that still have
+      // company go on: the wavefront waits for them anyway. (At most 1, 2, 4,
+      // 8 or any lane: 2 is fastest at 100,000 and 10,000 markets.)
+      if constexpr (EARLY) {
+        const int32_t looping = lanes_here();
+        if (budget != 0x7FFFFFFF && looping <= kEarlyStageLanes && s.bh != s.ah &&
+            (((int32_t)s.brec.x == 0 && (int32_t)s.arec.x > 0) ||
+             ((int32_t)s.arec.x == 0 && (int32_t)s.brec.x > 0)))
+          return false;
       }
     }
     // On the staged book a pass costs instructions, not memory round trips,
@@ -1320,7 +1352,8 @@ ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
 }
 
 // Fused add + match + BBO, one lane per market, in two passes.
-//   1. Every lane runs its market's loop for at most `budget` passes.
+//   1. Every lane runs its market's loop for at most `budget` passes (or
+//      fewer: see kEarlyStageLanes).
 //   2. Markets still crossing after that (long walks through stale or
 //      consumed orders) are finished one at a time: the whole wavefront copies
 //      the market's order records and level words into LDS with coalesced
@@ -1384,7 +1417,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     if (m < b.M && !(GAME && c.abort)) {
       sink.base = m * (int64_t)b.F;
       const GlobalBook gb{c.lv, c.rec};
-      if (match_loop<W, STATS>(st, c, gb, sink, out, bulk, budget)) {
+      if (match_loop<W, STATS, !GAME>(st, c, gb, sink, out, bulk, budget)) {
         quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, gb, ink.game, sok, &cy, last);
       } else {
         sink.flush(out, c.pf, c.C);  // frees the LDS for staging
@@ -1437,7 +1470,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
           LoopState<W> us = uniform_state(st);
           const MarketCtx uc = uniform_ctx(c);
           RowBuffer urb{rows, kStageRows, uni(rb.n), uni(rb.base)};
-          fin = match_loop<W, STATS>(us, uc, sb, urb, out, bulk, 0x7FFFFFFF) ? 1 : 0;
+          fin = match_loop<W, STATS, false>(us, uc, sb, urb, out, bulk, 0x7FFFFFFF) ? 1 : 0;
           st = us;
           rb.n = urb.n;
         }
@@ -1559,8 +1592,8 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
       if (GAME && c.abort) continue;
       sink.base = m * (int64_t)b.F;
       const GlobalBook gb{c.lv, c.rec};
-      const bool done = b.stats ? match_loop<W, true>(st, c, gb, sink, fo, bulk, budget)
-                                : match_loop<W, false>(st, c, gb, sink, fo, bulk, budget);
+      const bool done = b.stats ? match_loop<W, true, !GAME>(st, c, gb, sink, fo, bulk, budget)
+                                : match_loop<W, false, !GAME>(st, c, gb, sink, fo, bulk, budget);
       if (done) {
         if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok, cy,
                                                            last);
@@ -1574,8 +1607,8 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
         RowBuffer rb{rows.data(), kStageRows, 0, sink.base};
         bool fin = false;
         while (!fin) {
-          fin = b.stats ? match_loop<W, true>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF)
-                        : match_loop<W, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF);
+          fin = b.stats ? match_loop<W, true, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF)
+                        : match_loop<W, false, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF);
           flush_rows(fo, rows.data(), rb.n, rb.base, c.pf, c.C, 0, 1);
           rb.base += rb.n;
           rb.n = 0;
@@ -1745,7 +1778,7 @@ int default_stage_budget() {
     const int v = std::atoi(e);
     if (v >= 0) return v;
   }
-  return 12;
+  return 16;
 }
 
 int default_per_wave() {
