@@ -367,6 +367,20 @@ inline void write_bulk_host(const FillOut &out, const Bulk &bk) {
   }
 }
 
+// The fill row of one pass (market.cu:172-218): the earlier TID rests (ties go
+// to the ask side); price, quote size and quote TID are the resting order's.
+ASTRA_HD void make_row(const uint4 &b, const uint4 &a, int32_t qty, int32_t (&row)[8]) {
+  const bool bid_quote = (int32_t)b.z < (int32_t)a.z;
+  row[0] = (int32_t)((bid_quote ? b.w : a.w) & kNull16);
+  row[1] = qty;
+  row[2] = (int32_t)(bid_quote ? a.y : b.y);
+  row[3] = (int32_t)(bid_quote ? b.y : a.y);
+  row[4] = bid_quote ? 0 : 1;
+  row[5] = (int32_t)(bid_quote ? b.x : a.x);
+  row[6] = (int32_t)(bid_quote ? a.z : b.z);
+  row[7] = (int32_t)(bid_quote ? b.z : a.z);
+}
+
 // Portfolio update of one fill row (market.cu:221-232): the buyer is the bid
 // side's customer, i.e. the taker when the ask quotes and the quoter otherwise.
 // A self-trade or a zero quantity changes nothing, so it is skipped.
@@ -465,34 +479,45 @@ struct FillSink {
     for (int f = 0; f < 8; ++f) at(f, n) = row[f];
     if (++n == kRows) flush(out, pf, C);
   }
+
 };
 
-// Rows of the one market being finished on a staged book: [cap][8] words (LDS
-// on the GPU). When it is full the loop stops and the whole wavefront writes
-// the rows out (flush_rows), coalesced, then the loop resumes.
-constexpr int32_t kStageRows = 64;
+// Rows of the one market being finished on a staged book (LDS on the GPU),
+// kept short: {bid head slot | ask head slot << 16, quantity, the resting
+// order's size before the fill, 0}, one 16-byte write per row on the lane
+// that walks the book. The rest of a row (prices, customers, TIDs) is in the
+// two heads' records, which a walk never changes (it changes sizes only), so
+// the whole wavefront rebuilds the rows from the staged records when it writes
+// them out (flush_rows). When the buffer is full the walk stops, the rows go
+// out, and the walk resumes.
+constexpr int32_t kStageRows = 128;
 
 struct RowBuffer {
-  int32_t *rows;
+  uint4 *rows;
   int32_t cap;
   int32_t n;
   int64_t base;  // fill index of row 0
   ASTRA_HD bool full() const { return n == cap; }
-  ASTRA_HD void put(const FillOut &, int32_t *, int32_t, const int32_t (&row)[8]) {
-#pragma unroll
-    for (int f = 0; f < 8; ++f) rows[n * 8 + f] = row[f];
+  ASTRA_HD int32_t put_fill(const FillOut &, int32_t *, int32_t, const uint4 &b, const uint4 &a,
+                            uint32_t bh, uint32_t ah, int32_t qty) {
+    const bool bid_quote = (int32_t)b.z < (int32_t)a.z;  // as make_row
+    rows[n] = make_uint4(bh | (ah << 16), (uint32_t)qty, bid_quote ? b.x : a.x, 0u);
     ++n;
+    return (int32_t)((bid_quote ? b.w : a.w) & kNull16);
   }
 };
 
 // Rows [first, n) of a row buffer, `step` rows apart (64 lanes: row r by lane
-// r % 64, so each field's stores are coalesced), with their portfolio updates.
-ASTRA_HD void flush_rows(const FillOut &out, const int32_t *rows, int32_t n, int64_t base,
-                         int32_t *pf, int32_t C, int32_t first, int32_t step) {
+// r % 64, so each field's stores are coalesced), rebuilt from the staged
+// records `srec`, with their portfolio updates.
+ASTRA_HD void flush_rows(const FillOut &out, const uint4 *rows, const uint4 *srec, int32_t n,
+                         int64_t base, int32_t *pf, int32_t C, int32_t first, int32_t step) {
   for (int32_t r = first; r < n; r += step) {
+    const uint4 e = rows[r];
+    uint4 b = srec[e.x & kNull16], a = srec[e.x >> 16];
+    b.x = a.x = e.z;  // make_row takes the resting order's size from its record
     int32_t v[8];
-#pragma unroll
-    for (int f = 0; f < 8; ++f) v[f] = rows[r * 8 + f];
+    make_row(b, a, (int32_t)e.y, v);
     write_fill(out, base + r, v);
     apply_portfolio(pf, C, v[0], v[1], v[2], v[3], v[4] != 0);
   }
@@ -892,20 +917,6 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   s.zruns = s.zrows = 0;
 }
 
-// The fill row of one pass (market.cu:172-218): the earlier TID rests (ties go
-// to the ask side); price, quote size and quote TID are the resting order's.
-ASTRA_HD void make_row(const uint4 &b, const uint4 &a, int32_t qty, int32_t (&row)[8]) {
-  const bool bid_quote = (int32_t)b.z < (int32_t)a.z;
-  row[0] = (int32_t)((bid_quote ? b.w : a.w) & kNull16);
-  row[1] = qty;
-  row[2] = (int32_t)(bid_quote ? a.y : b.y);
-  row[3] = (int32_t)(bid_quote ? b.y : a.y);
-  row[4] = bid_quote ? 0 : 1;
-  row[5] = (int32_t)(bid_quote ? b.x : a.x);
-  row[6] = (int32_t)(bid_quote ? a.z : b.z);
-  row[7] = (int32_t)(bid_quote ? b.z : a.z);
-}
-
 // Passes in which one side's head has size 0 and the other side's a positive
 // size: the fill is 0, nothing but that head changes, and it moves to the next
 // order of its level (:237-256). Runs such passes back to back while the next
@@ -923,10 +934,7 @@ ASTRA_HD bool zero_walk(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, 
   for (;;) {
     const uint32_t nh = rec_next(w);
     if (nh >= (uint32_t)c.O || nh == h || s.fc >= c.F) break;  // NULL (or out of range) ends it
-    int32_t row[8];
-    make_row(s.brec, s.arec, 0, row);
-    sink.put(out, c.pf, c.C, row);
-    s.last_px = row[0];
+    s.last_px = sink.put_fill(out, c.pf, c.C, s.brec, s.arec, s.bh, s.ah, 0);
     ++s.fc;
     if (STATS) ++s.zrows;
     h = nh;
@@ -1032,8 +1040,10 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
       s.fc = -1;
       break;
     }
+    // In global memory the row is made here (kept in registers for the sink and
+    // the repeat cases); on a staged book the row buffer keeps a short form.
     int32_t row[8];
-    make_row(s.brec, s.arec, qty, row);
+    if constexpr (!BookMem::kStaged) make_row(s.brec, s.arec, qty, row);
     if (s.bh == s.ah && bsz != 0) {
       // One slot heads both sides with size s != 0: q = s, the slot becomes -s,
       // neither side pops, and the next pass is the same with -s. The fills
@@ -1042,8 +1052,12 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
       bulk.base = c.m * (int64_t)F + s.fc;
       bulk.count = F - s.fc;
       bulk.alt = 1;
+      if constexpr (BookMem::kStaged) {
+        make_row(s.brec, s.arec, qty, bulk.v);
+      } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) bulk.v[i] = row[i];
+        for (int i = 0; i < 8; ++i) bulk.v[i] = row[i];
+      }
       const int32_t fin = ((F - s.fc) & 1) ? (int32_t)(0u - (uint32_t)bsz) : bsz;
       bk.set_size(s.bh, fin);
       s.brec.x = s.arec.x = (uint32_t)fin;
@@ -1051,8 +1065,13 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
       if (STATS) ++s.forwarded;
       break;
     }
-    sink.put(out, c.pf, c.C, row);  // the row and its portfolio update (:198-232)
-    s.last_px = row[0];
+    // the row and its portfolio update (:198-232)
+    if constexpr (BookMem::kStaged) {
+      s.last_px = sink.put_fill(out, c.pf, c.C, s.brec, s.arec, s.bh, s.ah, qty);
+    } else {
+      sink.put(out, c.pf, c.C, row);
+      s.last_px = row[0];
+    }
     ++s.fc;
     // (:237-238) both decrements land on one slot when bid and ask alias
     if (s.bh == s.ah) {
@@ -1120,8 +1139,13 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
       bulk.base = c.m * (int64_t)F + s.fc;
       bulk.count = F - s.fc;
       bulk.alt = 0;
+      if constexpr (BookMem::kStaged) {
+        // (the heads and their records are the pass's: so is the row)
+        make_row(s.brec, s.arec, 0, bulk.v);
+      } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) bulk.v[i] = row[i];
+        for (int i = 0; i < 8; ++i) bulk.v[i] = row[i];
+      }
       s.fc = -1;
       if (STATS) ++s.forwarded;
       break;
@@ -1335,9 +1359,10 @@ constexpr size_t kSinkBytesPerWave = 8 * kRows * 64 * sizeof(int32_t);
 typedef __attribute__((address_space(1))) void gvoid_t;  // global memory
 typedef __attribute__((address_space(3))) void lvoid_t;  // LDS
 
-// Staged book of one market: records, level words, then its row buffer.
+// Staged book of one market: records, level words (padded to 16 bytes), then
+// its row buffer.
 inline size_t stage_bytes(int32_t L, int32_t O) {
-  return (size_t)O * 16 + (size_t)L * 8 + (size_t)kStageRows * 8 * sizeof(int32_t);
+  return (size_t)O * 16 + align_up((size_t)L * 8, 16) + (size_t)kStageRows * sizeof(uint4);
 }
 
 ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
@@ -1431,7 +1456,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
       const int64_t ms = shfl_i64(m, src);
       uint4 *srec = reinterpret_cast<uint4 *>(wave_lds);
       uint64_t *slv = reinterpret_cast<uint64_t *>(srec + b.O);
-      int32_t *rows = reinterpret_cast<int32_t *>(slv + b.L);
+      uint4 *rows = reinterpret_cast<uint4 *>(slv + ((b.L + 1) & ~1));  // 16-byte aligned
       uint4 *grec = b.records + ms * (int64_t)b.O;
       uint64_t *glv = reinterpret_cast<uint64_t *>(b.levels) + ms * (int64_t)b.L;
       int32_t *pfm = b.portfolios + ms * (int64_t)b.C * 2;
@@ -1480,7 +1505,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
         const int32_t n = __shfl(rb.n, src);
         const int64_t base = shfl_i64(rb.base, src);
         done = __shfl(fin, src) != 0;
-        flush_rows(out, rows, n, base, pfm, b.C, lane, 64);
+        flush_rows(out, rows, srec, n, base, pfm, b.C, lane, 64);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1572,7 +1597,7 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   (void)s;
   std::vector<uint4> srec(staged ? (size_t)h->O : 0);
   std::vector<uint16_t> slv(staged ? (size_t)h->L * 4 : 0);
-  std::vector<int32_t> rows((size_t)kStageRows * 8);
+  std::vector<uint4> rows((size_t)kStageRows);
   std::vector<Carry<W>> carry(MULTI ? (size_t)b.M : 0);
   for (auto &cy : carry) cy.state = cy.quotes = false;
   for (int32_t k = 0; k < (MULTI ? steps : 1); ++k) {
@@ -1609,7 +1634,7 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
         while (!fin) {
           fin = b.stats ? match_loop<W, true, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF)
                         : match_loop<W, false, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF);
-          flush_rows(fo, rows.data(), rb.n, rb.base, c.pf, c.C, 0, 1);
+          flush_rows(fo, rows.data(), srec.data(), rb.n, rb.base, c.pf, c.C, 0, 1);
           rb.base += rb.n;
           rb.n = 0;
         }
