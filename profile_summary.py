@@ -1,6 +1,6 @@
 """Reduce rocprofv3 CSV output of a bench.py run to the figures the bench reports.
 
-    python3 profile_summary.py trace  <dir> [--blocks 100,900,300,900]
+    python3 profile_summary.py trace  <dir> [--blocks 100,900,300,900] [--idle NAME,FIRST,COUNT]
     python3 profile_summary.py pmc    <dir> [--skip 100 --take 900]
     python3 profile_summary.py traffic <fetch dir> <write dir> \
         <copy fetch dir> <copy write dir> [--skip 100 --take 900]
@@ -9,6 +9,9 @@
 ``--kernel-trace --stats -f csv`` run and prints per-kernel durations, plus the
 mean of consecutive dispatch blocks of each kernel (bench.py issues its
 matching-kernel launches as warm-up W, timed K, latency replay, event replay).
+With ``--idle`` it also reports how much of the time from dispatch FIRST to
+dispatch FIRST + COUNT - 1 of the kernel whose name starts with NAME no kernel
+was running (the gaps between back-to-back launches), per dispatch.
 ``pmc`` prints per-dispatch means of every counter in ``*_counter_collection.csv``.
 ``traffic`` turns FETCH_SIZE and WRITE_SIZE (KiB per dispatch) into HBM bytes per
 launch, each scaled by what the same counter reads for bench.py's
@@ -41,7 +44,28 @@ def _short(name: str) -> str:
     return name.split("(")[0] if "(" in name else name
 
 
-def trace(dirpath: str, blocks: list[int]) -> str:
+def idle(disp: dict, name: str, first: int, count: int) -> str:
+    """Idle time on the GPU between the start of dispatch `first` and the end of
+    dispatch `first + count - 1` of kernel `name` (dispatches of every kernel in
+    between count as busy)."""
+    own = sorted(v for k, vs in disp.items() if k.startswith(name) for v in vs)
+    if len(own) < first + count:
+        return f"(fewer than {first + count} dispatches of {name})"
+    t0, t1 = own[first][0], own[first + count - 1][0] + own[first + count - 1][1]
+    spans = sorted((s, s + d) for vs in disp.values() for s, d in vs if s < t1 and s + d > t0)
+    busy, end = 0, t0
+    for s, e in spans:  # union of the kernels' intervals within [t0, t1]
+        s, e = max(s, end), min(e, t1)
+        if e > s:
+            busy += e - s
+            end = e
+    span = t1 - t0
+    return (f"From dispatch {first} to dispatch {first + count - 1} of `{name}`: {span / 1e3:.2f} us, "
+            f"of which no kernel ran {(span - busy) / 1e3:.2f} us ({(span - busy) / 1e3 / count:.2f} us "
+            f"per dispatch of `{name}`).")
+
+
+def trace(dirpath: str, blocks: list[int], gaps: str | None = None) -> str:
     out = []
     rows = list(csv.DictReader(open(_one(dirpath, "_kernel_stats.csv"))))
     out.append("| kernel | calls | average us | min us | max us | share |")
@@ -68,6 +92,9 @@ def trace(dirpath: str, blocks: list[int]) -> str:
             parts.append(f"[{i}, {i + len(seg)}): {statistics.mean(seg):.2f}")
             i += n
         out.append(f"- `{name}` ({len(d)} dispatches): " + "; ".join(parts))
+    if gaps:
+        name, first, count = gaps.rsplit(",", 2)
+        out += ["", idle(disp, name, int(first), int(count))]
     return "\n".join(out)
 
 
@@ -135,6 +162,7 @@ def main():
     t = sub.add_parser("trace")
     t.add_argument("dir")
     t.add_argument("--blocks", default="100,900,300,900")
+    t.add_argument("--idle", default=None, help="NAME,FIRST,COUNT: idle time between those dispatches")
     p = sub.add_parser("pmc")
     p.add_argument("dir")
     p.add_argument("--skip", type=int, default=100)
@@ -148,7 +176,7 @@ def main():
                    help="skip kernels launched fewer times (set-up fills)")
     a = ap.parse_args()
     if a.cmd == "trace":
-        print(trace(a.dir, [int(x) for x in a.blocks.split(",")]))
+        print(trace(a.dir, [int(x) for x in a.blocks.split(",")], a.idle))
     elif a.cmd == "pmc":
         print(pmc(a.dir, a.skip, a.take))
     else:

@@ -59,3 +59,15 @@ def test_matching_kernel_traffic_is_found_for_configs_2_and_4_driver_windows():
         traffic, src = bench.measured_traffic(cfg, cfg.M, cfg.bbo_every_step, _window(cfg.steps))
         assert src == f"profiles/quote_match_config{idx}_{name}_window.md", src
         assert traffic is not None and traffic > 0
+
+
+def test_profile_summary_idle_counts_only_time_no_kernel_ran():
+    import profile_summary as ps
+    # matching kernel 70 ns, a 2 ns gap, bbo 4 ns, a 4 ns gap, matching again (times in ns)
+    disp = {"void quote_match_kernel<2>": [(0, 70), (80, 70), (160, 70)],
+            "bbo_kernel": [(72, 4), (152, 4)]}
+    line = ps.idle(disp, "void quote_match_kernel", 0, 3)
+    assert "0.23 us, of which no kernel ran 0.01 us" in line  # 230 ns span, 12 ns idle
+    # overlapping spans are counted once
+    disp = {"a": [(0, 100), (50, 100)], "b": [(120, 10)]}
+    assert "no kernel ran 0.00 us" in ps.idle(disp, "a", 0, 2)
