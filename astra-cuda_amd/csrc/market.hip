@@ -113,7 +113,10 @@ struct astra_market {
   int block;                  // launch block size of the per-market kernels
   int32_t stage_budget;       // loop passes before a market is staged in LDS (0: never)
   int32_t lds_limit;          // LDS bytes a workgroup may use on the device
+  int32_t lds_per_cu;         // LDS bytes of one CU
+  int32_t cus;                // CUs of the device
   int32_t per_wave;           // markets per wavefront of the matching kernel (0: default)
+  int32_t fill_rows;          // fill rows a lane buffers before writing them (0: by grid)
   unsigned long long *stats;  // see astra_market_set_stats
   char *ws;
   size_t ws_bytes;
@@ -400,19 +403,20 @@ ASTRA_HD void apply_portfolio(int32_t *pf, int32_t C, int32_t price, int32_t qty
 // Fill rows a lane has produced but not yet written. On the GPU the rows live
 // in LDS as [field][row][lane] (a row write by 64 lanes touches 64 consecutive
 // words: no bank conflicts); the host build keeps them in a local array. Rows
-// go out kRows at a time as aligned vector stores (rows k..k+kRows-1 of one
-// market are contiguous in each field array), together with the portfolio
-// updates they imply. Nothing beyond the call's last row is ever written: the
-// reference leaves later entries of a FillBatch untouched.
-constexpr int kRows = 4;
-
+// go out R at a time (2 or 4, a template argument of the matching kernel) as
+// aligned vector stores (rows k..k+R-1 of one market are contiguous in each
+// field array), together with the portfolio updates they imply. Nothing beyond
+// the call's last row is ever written: the reference leaves later entries of a
+// FillBatch untouched.
+template <int R>
 struct FillSink {
+  static_assert(R == 2 || R == 4, "two or four rows");
 #if defined(__HIP_DEVICE_COMPILE__)
-  int32_t *lds;  // this wavefront's [8][kRows][64] buffer
+  int32_t *lds;  // this wavefront's [8][R][64] buffer
   int lane;
-  __device__ int32_t &at(int f, int r) const { return lds[(f * kRows + r) * 64 + lane]; }
+  __device__ int32_t &at(int f, int r) const { return lds[(f * R + r) * 64 + lane]; }
 #else
-  mutable int32_t buf[8][kRows];
+  mutable int32_t buf[8][R];
   int32_t &at(int f, int r) const { return buf[f][r]; }
 #endif
   int64_t base = 0;  // fill index of buffered row 0
@@ -440,19 +444,23 @@ struct FillSink {
     for (int j = 0; j < 7; ++j) {
       int32_t *d = dst32[j] + base;
       const int f = fidx[j];
-      if ((reinterpret_cast<uintptr_t>(d) & 15) == 0) {
+      const uintptr_t a = reinterpret_cast<uintptr_t>(d);
+      if (R == 4 && (a & 15) == 0) {  // rows k..k+3 of a 4-row-aligned run
         if (n == 4) {
           gst(reinterpret_cast<int4 *>(d), make_int4(at(f, 0), at(f, 1), at(f, 2), at(f, 3)));
         } else {
           if (n & 2) gst(reinterpret_cast<int2 *>(d), make_int2(at(f, 0), at(f, 1)));
           if (n & 1) gst(d + (n - 1), at(f, n - 1));
         }
+      } else if (R == 2 && n == 2 && (a & 7) == 0) {
+        gst(reinterpret_cast<int2 *>(d), make_int2(at(f, 0), at(f, 1)));
       } else {
         for (int r = 0; r < n; ++r) gst(d + r, at(f, r));
       }
     }
     uint8_t *d8 = out.is_sell_quote + base;
-    if ((reinterpret_cast<uintptr_t>(d8) & 3) == 0) {
+    const uintptr_t a8 = reinterpret_cast<uintptr_t>(d8);
+    if (R == 4 && (a8 & 3) == 0) {
       if (n == 4) {
         gst(reinterpret_cast<uint32_t *>(d8),
             (uint32_t)at(4, 0) | ((uint32_t)at(4, 1) << 8) | ((uint32_t)at(4, 2) << 16) |
@@ -463,6 +471,8 @@ struct FillSink {
               (uint16_t)((uint32_t)at(4, 0) | ((uint32_t)at(4, 1) << 8)));
         if (n & 1) gst(d8 + (n - 1), (uint8_t)at(4, n - 1));
       }
+    } else if (R == 2 && n == 2 && (a8 & 1) == 0) {
+      gst(reinterpret_cast<uint16_t *>(d8), (uint16_t)((uint32_t)at(4, 0) | ((uint32_t)at(4, 1) << 8)));
     } else {
       for (int r = 0; r < n; ++r) gst(d8 + r, (uint8_t)at(4, r));
     }
@@ -477,7 +487,7 @@ struct FillSink {
   ASTRA_HD void put(const FillOut &out, int32_t *pf, int32_t C, const int32_t (&row)[8]) {
 #pragma unroll
     for (int f = 0; f < 8; ++f) at(f, n) = row[f];
-    if (++n == kRows) flush(out, pf, C);
+    if (++n == R) flush(out, pf, C);
   }
 
 };
@@ -1158,9 +1168,9 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
 // position, and the best levels of the book as left (prices into the
 // workspace's BBO cache, head slots into tob: what get_bbo_kernel,
 // market.cu:280-320, would find). STATS also adds the call's work counts.
-template <int W, bool STATS, bool GAME, bool MULTI, class BookMem>
+template <int W, bool STATS, bool GAME, bool MULTI, class BookMem, class Sink>
 ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx &c,
-                             const LoopState<W> &s, FillSink &sink, const BookMem &bk,
+                             const LoopState<W> &s, Sink &sink, const BookMem &bk,
                              const GameMove &game, const StepOut &so,
                              Carry<W> *cy = nullptr, bool last = true) {
   const int64_t M = b.M, m = c.m;
@@ -1353,9 +1363,11 @@ __device__ __forceinline__ void write_bulk_wave(const FillOut &out, const Bulk &
 }
 
 // All 64 lanes of a wavefront reach write_bulk_wave (no early return).
-// LDS per wavefront: the fill-row buffer during the first pass, then (when
-// staging is enabled for the shape) the staged book of one market.
-constexpr size_t kSinkBytesPerWave = 8 * kRows * 64 * sizeof(int32_t);
+// LDS per wavefront: the fill-row buffer and (when staging is enabled for the
+// shape) the staged book of one market, side by side where the whole grid
+// still fits on the CUs that way, else sharing one area (the book overwrites
+// the buffer after the lanes have written their rows out).
+ASTRA_HD constexpr size_t sink_bytes(int32_t rows) { return (size_t)8 * rows * 64 * sizeof(int32_t); }
 typedef __attribute__((address_space(1))) void gvoid_t;  // global memory
 typedef __attribute__((address_space(3))) void lvoid_t;  // LDS
 
@@ -1386,12 +1398,21 @@ ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
 // MULTI runs `steps` consecutive calls in one launch: markets are independent,
 // so each wavefront goes on to its markets' next step as soon as it is done
 // with this one, with no grid-wide wait between steps.
+// FR: fill rows a lane buffers before writing them (fill_rows_per_flush). With
+// FR = 2 (small grids) a staged book has LDS of its own beside the row buffer,
+// and the finished lanes' epilogues come after the staged walks: a staged
+// book's copy-in ends with a wait for every memory operation the wavefront has
+// in flight (loads and stores share one counter), so stores issued before it
+// delay it. With FR = 4 the book reuses the row buffer's LDS (the whole grid of
+// a large launch fits on the CUs only that way), so the finished lanes write
+// their epilogues, rows included, before it.
 // All 64 lanes of a wavefront reach the ballots (no early return).
-template <int W, bool STATS, bool GAME, bool MULTI, bool ROWS>
+template <int W, bool STATS, bool GAME, bool MULTI, bool ROWS, int FR>
 __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, FillOut out,
                                                           StepOut so, int32_t steps,
                                                           int32_t budget, int32_t wave_words,
                                                           int32_t per_wave) {
+  constexpr bool kApart = FR == 2;  // the staged book beside the row buffer
   extern __shared__ int32_t lds_words[];
   // The FillBatch layout is a template argument: the other layout's pointers
   // become constant nulls, so their code and registers drop out.
@@ -1420,7 +1441,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
   const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64;
   const int64_t m = lane < per_wave ? wave * per_wave + lane : b.M;
   int32_t *wave_lds = lds_words + uni((int32_t)(threadIdx.x / 64) * wave_words);
-  FillSink sink;
+  FillSink<FR> sink;
 #if defined(__HIP_DEVICE_COMPILE__)
   sink.lds = wave_lds;
   sink.lane = lane;
@@ -1436,16 +1457,19 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     bulk.count = 0;
     MarketCtx c;
     LoopState<W> st;
-    bool suspended = false;
+    bool suspended = false, finished = false;
     if (m < b.M) quote_prologue<W, GAME, MULTI>(b, ink, m, c, st, &cy);
     if (MULTI && m < b.M) load_next_quotes(in, b.M, k + 1, steps, m, cy);
     if (m < b.M && !(GAME && c.abort)) {
       sink.base = m * (int64_t)b.F;
       const GlobalBook gb{c.lv, c.rec};
       if (match_loop<W, STATS, !GAME>(st, c, gb, sink, out, bulk, budget)) {
-        quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, gb, ink.game, sok, &cy, last);
+        if constexpr (kApart)
+          finished = true;
+        else
+          quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, gb, ink.game, sok, &cy, last);
       } else {
-        sink.flush(out, c.pf, c.C);  // frees the LDS for staging
+        sink.flush(out, c.pf, c.C);  // the staged walk's rows follow these
         suspended = true;
       }
     }
@@ -1454,7 +1478,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
       const int src = __ffsll((unsigned long long)todo) - 1;
       todo &= todo - 1;
       const int64_t ms = shfl_i64(m, src);
-      uint4 *srec = reinterpret_cast<uint4 *>(wave_lds);
+      uint4 *srec = reinterpret_cast<uint4 *>(wave_lds + (kApart ? sink_bytes(FR) / 4 : 0));
       uint64_t *slv = reinterpret_cast<uint64_t *>(srec + b.O);
       uint4 *rows = reinterpret_cast<uint4 *>(slv + ((b.L + 1) & ~1));  // 16-byte aligned
       uint4 *grec = b.records + ms * (int64_t)b.O;
@@ -1525,6 +1549,11 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+    if constexpr (kApart) {
+      if (finished)
+        quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, GlobalBook{c.lv, c.rec},
+                                              ink.game, sok, &cy, last);
+    }
     write_bulk_wave(out, bulk);
     if (MULTI) {  // this step's rows and book writes come before the next step's
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1582,6 +1611,19 @@ int32_t markets_per_wave(const astra_market *h, bool game) {
   return (game && h->M <= 32 * 2048) ? 32 : 64;
 }
 
+// Fill rows a lane buffers before writing them: 2 where each CU holds at most
+// two of the grid's wavefronts, 4 above. Under light load the rows that remain
+// buffered at the end of a lane's chain are stores its wavefront waits out at
+// the end; flushing every 2 rows leaves fewer (with the staged book's own LDS
+// and the deferred epilogues: -5% after the ring wraps at 10,000 markets of the
+// config-3 shape, -3% at config 4, -7.5% for the config-5 game move). Under
+// full load every flush inside the loop costs the whole wavefront issue slots
+// (+10% before the ring wraps at 100,000 markets), so 4 there.
+int32_t fill_rows_per_flush(const astra_market *h, int64_t waves_per_cu) {
+  if (h->fill_rows) return h->fill_rows;
+  return waves_per_cu <= 2 ? 2 : 4;
+}
+
 template <int W, bool GAME, bool MULTI>
 int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &fo,
                        const StepOut &so, int32_t steps, hipStream_t s) {
@@ -1593,6 +1635,17 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
                       (size_t)(h->block / 64) * align_up(stage_bytes(h->L, h->O), 16) <=
                           (size_t)h->lds_limit;
   const int32_t budget = staged ? h->stage_budget : 0x7FFFFFFF;
+  const int32_t per_wave = markets_per_wave(h, GAME);
+  const int64_t waves = ((int64_t)b.M + per_wave - 1) / per_wave;
+  const int64_t waves_per_cu = (waves + h->cus - 1) / h->cus;
+  const size_t stage_b = staged ? align_up(stage_bytes(h->L, h->O), 16) : (size_t)0;
+  // (a multi-step launch buffers 4: its wavefronts go on to the next step; and 2
+  // only where the staged book fits beside the row buffer for every wavefront
+  // the grid puts on a CU)
+  const size_t apart_block = (size_t)(h->block / 64) * (sink_bytes(2) + stage_b);
+  const bool fits_apart = apart_block <= (size_t)h->lds_limit &&
+                          (int64_t)((size_t)h->lds_per_cu / apart_block) * (h->block / 64) >= waves_per_cu;
+  const int32_t rows_cap = (MULTI || !fits_apart) ? 4 : fill_rows_per_flush(h, waves_per_cu);
 #ifdef ASTRA_HOST_EMULATION
   (void)s;
   std::vector<uint4> srec(staged ? (size_t)h->O : 0);
@@ -1600,74 +1653,88 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   std::vector<uint4> rows((size_t)kStageRows);
   std::vector<Carry<W>> carry(MULTI ? (size_t)b.M : 0);
   for (auto &cy : carry) cy.state = cy.quotes = false;
+  // one market's call, with a fill-row buffer of the launch's depth
+  auto market = [&](auto sink, const QuoteIn &ink, const StepOut &sok, int32_t k, bool last,
+                    int64_t m) {
+    Bulk bulk;
+    bulk.count = 0;
+    MarketCtx c;
+    LoopState<W> st;
+    Carry<W> *cy = MULTI ? &carry[(size_t)m] : nullptr;
+    quote_prologue<W, GAME, MULTI>(b, ink, m, c, st, cy);
+    if (MULTI) load_next_quotes(in, b.M, k + 1, steps, m, *cy);
+    if (GAME && c.abort) return;
+    sink.base = m * (int64_t)b.F;
+    const GlobalBook gb{c.lv, c.rec};
+    const bool done = b.stats ? match_loop<W, true, !GAME>(st, c, gb, sink, fo, bulk, budget)
+                              : match_loop<W, false, !GAME>(st, c, gb, sink, fo, bulk, budget);
+    if (done) {
+      if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok, cy, last);
+      else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok, cy, last);
+    } else {  // the second pass, as on the GPU
+      sink.flush(fo, c.pf, c.C);
+      std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
+      std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
+      const StagedBook sb{slv.data(), srec.data()};
+      RowBuffer rb{rows.data(), kStageRows, 0, sink.base};
+      bool fin = false;
+      while (!fin) {
+        fin = b.stats ? match_loop<W, true, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF)
+                      : match_loop<W, false, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF);
+        flush_rows(fo, rows.data(), srec.data(), rb.n, rb.base, c.pf, c.C, 0, 1);
+        rb.base += rb.n;
+        rb.n = 0;
+      }
+      std::memcpy(c.rec, srec.data(), (size_t)h->O * 16);
+      std::memcpy(c.lv, slv.data(), (size_t)h->L * 8);
+      sink.base = rb.base;
+      if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok, cy, last);
+      else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok, cy, last);
+    }
+    if (bulk.count > 0) write_bulk_host(fo, bulk);
+  };
   for (int32_t k = 0; k < (MULTI ? steps : 1); ++k) {
     QuoteIn ink = in;
     StepOut sok = so;
     if (MULTI) step_views(in, so, b.M, steps, k, ink, sok);
     const bool last = k + 1 == (MULTI ? steps : 1);
     for (int64_t m = 0; m < b.M; ++m) {
-      Bulk bulk;
-      bulk.count = 0;
-      FillSink sink;
-      MarketCtx c;
-      LoopState<W> st;
-      Carry<W> *cy = MULTI ? &carry[(size_t)m] : nullptr;
-      quote_prologue<W, GAME, MULTI>(b, ink, m, c, st, cy);
-      if (MULTI) load_next_quotes(in, b.M, k + 1, steps, m, *cy);
-      if (GAME && c.abort) continue;
-      sink.base = m * (int64_t)b.F;
-      const GlobalBook gb{c.lv, c.rec};
-      const bool done = b.stats ? match_loop<W, true, !GAME>(st, c, gb, sink, fo, bulk, budget)
-                                : match_loop<W, false, !GAME>(st, c, gb, sink, fo, bulk, budget);
-      if (done) {
-        if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok, cy,
-                                                           last);
-        else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok, cy,
-                                                         last);
-      } else {  // the second pass, as on the GPU
-        sink.flush(fo, c.pf, c.C);
-        std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
-        std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
-        const StagedBook sb{slv.data(), srec.data()};
-        RowBuffer rb{rows.data(), kStageRows, 0, sink.base};
-        bool fin = false;
-        while (!fin) {
-          fin = b.stats ? match_loop<W, true, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF)
-                        : match_loop<W, false, false>(st, c, sb, rb, fo, bulk, 0x7FFFFFFF);
-          flush_rows(fo, rows.data(), srec.data(), rb.n, rb.base, c.pf, c.C, 0, 1);
-          rb.base += rb.n;
-          rb.n = 0;
-        }
-        std::memcpy(c.rec, srec.data(), (size_t)h->O * 16);
-        std::memcpy(c.lv, slv.data(), (size_t)h->L * 8);
-        sink.base = rb.base;
-        if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok, cy,
-                                                           last);
-        else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok, cy,
-                                                         last);
-      }
-      if (bulk.count > 0) write_bulk_host(fo, bulk);
+      if (rows_cap == 2) market(FillSink<2>{}, ink, sok, k, last, m);
+      else market(FillSink<4>{}, ink, sok, k, last, m);
     }
   }
 #else
-  const size_t wave_bytes =
-      std::max(kSinkBytesPerWave, staged ? align_up(stage_bytes(h->L, h->O), 16) : (size_t)0);
+  const size_t sink_b = sink_bytes(rows_cap);
+  const size_t wave_bytes = rows_cap == 2 ? sink_b + stage_b : std::max(sink_b, stage_b);
   const size_t lds = (size_t)(h->block / 64) * wave_bytes;
   const int32_t wave_words = (int32_t)(wave_bytes / 4);
-  const int32_t per_wave = markets_per_wave(h, GAME);
   const unsigned grid = grid_for(((int64_t)b.M + per_wave - 1) / per_wave * 64, h->block);
+  // (the counting kernels buffer 4 rows whatever the grid: their results are the
+  // same, and one depth keeps their number down)
   if (b.stats && fo.rows)
-    hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI, true>), dim3(grid), dim3(h->block),
-                       lds, s, b, in, fo, so, steps, budget, wave_words, per_wave);
+    hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI, true, 4>), dim3(grid),
+                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
+                       per_wave);
   else if (b.stats)
-    hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI, false>), dim3(grid), dim3(h->block),
-                       lds, s, b, in, fo, so, steps, budget, wave_words, per_wave);
+    hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI, false, 4>), dim3(grid),
+                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
+                       per_wave);
+  else if (fo.rows && rows_cap == 2 && !MULTI)
+    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, true, MULTI ? 4 : 2>), dim3(grid),
+                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
+                       per_wave);
   else if (fo.rows)
-    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, true>), dim3(grid),
-                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words, per_wave);
+    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, true, 4>), dim3(grid),
+                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
+                       per_wave);
+  else if (rows_cap == 2 && !MULTI)
+    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, false, MULTI ? 4 : 2>), dim3(grid),
+                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
+                       per_wave);
   else
-    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, false>), dim3(grid),
-                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words, per_wave);
+    hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, false, 4>), dim3(grid),
+                       dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
+                       per_wave);
 #endif
   ASTRA_HIP_CHECK(rt_last_error(), "AddTwoSidedQuotes");
   return ASTRA_OK;
@@ -1812,6 +1879,14 @@ int default_per_wave() {
   return (x >= 1 && x <= 64) ? x : 0;
 }
 
+// ASTRA_MARKET_FILL_ROWS (2 or 4) fixes the fill rows a lane of the matching
+// kernel buffers before writing them out; else fill_rows_per_flush decides.
+int32_t default_fill_rows() {
+  const char *e = std::getenv("ASTRA_MARKET_FILL_ROWS");
+  const int x = e ? std::atoi(e) : 0;
+  return (x == 2 || x == 4) ? x : 0;
+}
+
 int default_block() {
   const char *e = std::getenv("ASTRA_MARKET_BLOCK");
   if (e) {
@@ -1873,8 +1948,10 @@ int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, i
   ASTRA_ABI_CHECK(workspace_bytes, >=, lay.total);
   DeviceGuard g(device_id);
   if (!g.ok) return fail(ASTRA_ERR_HIP, "hipSetDevice failed");
-  int lds_limit = 0;
+  int lds_limit = 0, lds_per_cu = 0, cus = 0;
   ASTRA_HIP_CHECK(rt_lds_per_block(device_id, &lds_limit), "hipDeviceGetAttribute");
+  ASTRA_HIP_CHECK(rt_lds_per_cu(device_id, &lds_per_cu), "hipDeviceGetAttribute");
+  ASTRA_HIP_CHECK(rt_cu_count(device_id, &cus), "hipDeviceGetAttribute");
   astra_market *h = new astra_market();
   h->M = M;
   h->L = L;
@@ -1888,7 +1965,10 @@ int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, i
   h->block = default_block();
   h->stage_budget = default_stage_budget();
   h->lds_limit = lds_limit;
+  h->lds_per_cu = lds_per_cu > 0 ? lds_per_cu : lds_limit;
+  h->cus = cus > 0 ? cus : 1;
   h->per_wave = default_per_wave();
+  h->fill_rows = default_fill_rows();
   h->stats = nullptr;
   h->ws = static_cast<char *>(workspace);
   h->ws_bytes = workspace_bytes;

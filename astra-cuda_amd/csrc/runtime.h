@@ -36,9 +36,18 @@ inline hipError_t rt_memcpy(void *d, const void *s, size_t n, hipStream_t) {
 }
 inline hipError_t rt_sync(hipStream_t) { return hipSuccess; }
 inline hipError_t rt_last_error() { return hipSuccess; }
-// The host build stands in for gfx950, whose workgroups may use 160 KB of LDS.
+// The host build stands in for gfx950: 256 CUs with 160 KB of LDS each, all of
+// which one workgroup may use.
 inline hipError_t rt_lds_per_block(int, int *bytes) {
   *bytes = 160 * 1024;
+  return hipSuccess;
+}
+inline hipError_t rt_lds_per_cu(int, int *bytes) {
+  *bytes = 160 * 1024;
+  return hipSuccess;
+}
+inline hipError_t rt_cu_count(int, int *n) {
+  *n = 256;
   return hipSuccess;
 }
 struct DeviceGuard {
@@ -60,6 +69,12 @@ inline hipError_t rt_sync(hipStream_t st) { return hipStreamSynchronize(st); }
 inline hipError_t rt_last_error() { return hipGetLastError(); }
 inline hipError_t rt_lds_per_block(int dev, int *bytes) {
   return hipDeviceGetAttribute(bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+}
+inline hipError_t rt_lds_per_cu(int dev, int *bytes) {
+  return hipDeviceGetAttribute(bytes, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev);
+}
+inline hipError_t rt_cu_count(int dev, int *n) {
+  return hipDeviceGetAttribute(n, hipDeviceAttributeMultiprocessorCount, dev);
 }
 // Restores the calling thread's current device when it goes out of scope.
 struct DeviceGuard {

@@ -111,16 +111,18 @@ def compare_portfolios(gpu_mk, ora_mk, where: str):
         raise AssertionError(f"{where}: portfolios differ at {bad.tolist()}")
 
 
-def make_market(M, L, O, F, C, extended=None, stage_budget=None, per_wave=None):
+def make_market(M, L, O, F, C, extended=None, stage_budget=None, per_wave=None, fill_rows=None):
     """VecMarket through the drop-in API. stage_budget (read by the engine when the
     market is created) sets the loop passes before a market's book is staged in
     LDS; 1 forces the staged path for every market that crosses twice. per_wave
-    (likewise) sets the markets per wavefront of the matching kernel."""
+    (likewise) sets the markets per wavefront of the matching kernel, fill_rows
+    (2 or 4) the fill rows a lane buffers before writing them."""
     import os
     from astra_cuda import order_matching as aom
     if extended is None:
         extended = L > 128 or O > 1024 or F > 1024 or C > 1024
-    env = {"ASTRA_MARKET_STAGE_BUDGET": stage_budget, "ASTRA_MARKET_PER_WAVE": per_wave}
+    env = {"ASTRA_MARKET_STAGE_BUDGET": stage_budget, "ASTRA_MARKET_PER_WAVE": per_wave,
+           "ASTRA_MARKET_FILL_ROWS": fill_rows}
     old = {k: os.environ.get(k) for k in env}
     for k, v in env.items():
         if v is not None:
@@ -139,14 +141,14 @@ def make_market(M, L, O, F, C, extended=None, stage_budget=None, per_wave=None):
 
 def run_parity(M, L, O, F, C, steps, gen, *, bbo_every=1, full_every=0, last_every=1,
                extended=None, nthreads=8, label="", stage_budget=None, layout="columns",
-               per_wave=None):
+               per_wave=None, fill_rows=None):
     """Drive GPU engine and oracle with the same inputs; compare after every step.
 
     ``gen(t)`` returns (bid_px, bid_sz, ask_px, ask_sz, cust) int32 arrays of shape [M].
     Returns summary statistics (fill rows compared, overflows seen).
     """
     from oracle.oracle import OracleMarket
-    g = make_market(M, L, O, F, C, extended, stage_budget, per_wave)
+    g = make_market(M, L, O, F, C, extended, stage_budget, per_wave, fill_rows)
     gf, gb = g.new_fill_batch(layout), g.new_bbo_batch()
     o = OracleMarket(M, L, O, F, C)
     of, ob = o.new_fill_batch(), o.new_bbo_batch()

@@ -38,10 +38,12 @@ def _compare(em, ef, eb, om, of, ob, F, where):
     assert np.array_equal(em.portfolios, om.customer_portfolios), where
 
 
-def _emu(M, L, O, F, C, stage_budget=None, extended=None):
+def _emu(M, L, O, F, C, stage_budget=None, extended=None, fill_rows=None):
     """Emulated engine; stage_budget sets the passes before a market's book is staged
-    (0: never), read by the engine when the market is created."""
-    env = {"ASTRA_MARKET_STAGE_BUDGET": stage_budget}
+    (0: never), fill_rows (2 or 4) the fill rows a lane buffers before writing them
+    (by default 2 for grids this small), both read by the engine when the market is
+    created."""
+    env = {"ASTRA_MARKET_STAGE_BUDGET": stage_budget, "ASTRA_MARKET_FILL_ROWS": fill_rows}
     old = {k: os.environ.get(k) for k in env}
     try:
         for k, v in env.items():
@@ -57,8 +59,8 @@ def _emu(M, L, O, F, C, stage_budget=None, extended=None):
 
 
 def _run(M, L, O, F, C, steps, gen, with_stats=False, stage_budget=None, layout="columns",
-         extended=None):
-    em, om = _emu(M, L, O, F, C, stage_budget, extended), OracleMarket(M, L, O, F, C)
+         extended=None, fill_rows=None):
+    em, om = _emu(M, L, O, F, C, stage_budget, extended, fill_rows), OracleMarket(M, L, O, F, C)
     ef, of = em.new_fill_batch(layout), om.new_fill_batch()
     eb, ob = em.new_bbo_batch(), om.new_bbo_batch()
     stats = np.zeros(10, np.int64)
@@ -102,10 +104,12 @@ ALIAS_CASES = [
 ]
 
 
-@pytest.mark.parametrize("stage_budget,layout", [(None, "columns"), (0, "columns"), (1, "columns"),
-                                                 (3, "columns"), (None, "rows"), (1, "rows")])
+@pytest.mark.parametrize("stage_budget,layout,fill_rows",
+                         [(None, "columns", None), (0, "columns", None), (1, "columns", None),
+                          (3, "columns", None), (None, "rows", None), (1, "rows", None),
+                          (None, "columns", 4), (1, "rows", 4)])
 @pytest.mark.parametrize("M,L,O,F,C,steps,seed", ALIAS_CASES)
-def test_emulated_aliasing_vs_oracle(M, L, O, F, C, steps, seed, stage_budget, layout):
+def test_emulated_aliasing_vs_oracle(M, L, O, F, C, steps, seed, stage_budget, layout, fill_rows):
     rng = np.random.default_rng(seed)
     hot = max(4, min(L, 24))
 
@@ -118,7 +122,8 @@ def test_emulated_aliasing_vs_oracle(M, L, O, F, C, steps, seed, stage_budget, l
         return (bid, rng.integers(-1, 8, M).astype(np.int32), ask,
                 rng.integers(-1, 8, M).astype(np.int32), rng.integers(-1, C + 2, M).astype(np.int32))
 
-    _, _, st = _run(M, L, O, F, C, steps, gen, with_stats=True, stage_budget=stage_budget, layout=layout)
+    _, _, st = _run(M, L, O, F, C, steps, gen, with_stats=True, stage_budget=stage_budget, layout=layout,
+                    fill_rows=fill_rows)
     # tiny rings exercise both overflow routes: the repeating-state fast-forward
     # and the ordinary F-th fill (with O = 1 every overflow repeats)
     assert st["fast_forwards"] > 0
@@ -143,14 +148,15 @@ def test_emulated_config1_full_run():
     assert st["fills"] > 0
 
 
-@pytest.mark.parametrize("stage_budget,layout", [(None, "columns"), (1, "columns"), (1, "rows")])
-def test_emulated_config3_and_4_samples(stage_budget, layout):
+@pytest.mark.parametrize("stage_budget,layout,fill_rows", [(None, "columns", None), (1, "columns", None),
+                                                           (1, "rows", None), (None, "columns", 4)])
+def test_emulated_config3_and_4_samples(stage_budget, layout, fill_rows):
     from astra_cuda.workloads import CONFIGS, QuoteStream
     for idx, M, steps in ((3, 300, 700), (4, 60, 400)):
         cfg = CONFIGS[idx]
         qs = QuoteStream(cfg, np.arange(M))
         _run(M, cfg.L, cfg.O, cfg.F, cfg.C, steps, qs.step, with_stats=True, stage_budget=stage_budget,
-             layout=layout)
+             layout=layout, fill_rows=fill_rows)
 
 
 def test_emulated_reset_clear_clone_to_string():

@@ -96,10 +96,11 @@ ALIAS_CASES = [
 ]
 
 
-@pytest.mark.parametrize("stage_budget,layout", [(None, "columns"), (1, "columns"), (1, "rows")])
+@pytest.mark.parametrize("stage_budget,layout,fill_rows", [(None, "columns", None), (1, "columns", None),
+                                                           (1, "rows", None), (1, "columns", 4)])
 @pytest.mark.parametrize("M,L,O,F,C,steps,seed", ALIAS_CASES)
-def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, layout):
-    _log(f"aliasing M={M} L={L} O={O} F={F} stage budget {stage_budget} {layout}")
+def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, layout, fill_rows):
+    _log(f"aliasing M={M} L={L} O={O} F={F} stage budget {stage_budget} {layout} fill rows {fill_rows}")
     rng = np.random.default_rng(seed)
     hot = max(4, min(L, 24))  # concentrate prices so books cross often
 
@@ -113,7 +114,7 @@ def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, lay
                 rng.integers(-1, 8, M).astype(np.int32), rng.integers(-1, C + 2, M).astype(np.int32))
 
     r = run_parity(M, L, O, F, C, steps, gen, full_every=50, label=f"alias L{L} O{O}",
-                   stage_budget=stage_budget, layout=layout)
+                   stage_budget=stage_budget, layout=layout, fill_rows=fill_rows)
     if O <= 3:
         assert r["overflows"] > 0
 
