@@ -615,14 +615,19 @@ def profile_traffic(prefix: str, kernel: str, window):
     committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/ whose name
     starts with `prefix` (copy-calibrated), or (None, None) when no summary holds a
     figure for exactly that window (traffic depends on the book's state, so a
-    figure from other steps would describe other work)."""
+    figure from other steps would describe other work). `kernel` is the name up to
+    its closing '>'; the matching kernel's last template argument, the fill rows a
+    lane buffers (2 or 4), is the engine's choice for the grid and may follow."""
     import glob
-    key = f"traffic_bytes_per_launch[void {kernel}][{window[0]},{window[1]}]:"
+    import re
+    key = re.compile(r"traffic_bytes_per_launch\[void " + re.escape(kernel) + r"(, [24])?>\]\["
+                     + f"{window[0]},{window[1]}" + r"\]:\s*(\S+)")
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", prefix + "*.md"))):
         with open(path) as f:
             for line in f:
-                if line.startswith(key):
-                    return float(line.split(":", 1)[1]), os.path.relpath(path, ROOT)
+                m = key.match(line)
+                if m:
+                    return float(m.group(2)), os.path.relpath(path, ROOT)
     return None, None
 
 
@@ -635,7 +640,7 @@ def measured_traffic(cfg, M, bbo, window):
     while words * 64 < cfg.L:
         words *= 2
     return profile_traffic(f"quote_match_config{cfg.index}_{cfg.name}_",
-                           f"quote_match_kernel<{words}, false, false, false, false>", window)
+                           f"quote_match_kernel<{words}, false, false, false, false", window)
 
 
 def game_traffic(cfg, N, window):
@@ -644,7 +649,7 @@ def game_traffic(cfg, N, window):
     if N != cfg.envs:
         return None, None
     return profile_traffic(f"game_move_config5_{cfg.name}_",
-                           "quote_match_kernel<2, false, true, false, true>", window)
+                           "quote_match_kernel<2, false, true, false, true", window)
 
 
 def cpu_baseline(args, cfg, host, M, T0, K, bbo):
