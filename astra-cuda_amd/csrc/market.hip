@@ -597,8 +597,10 @@ ASTRA_HD void load_next_quotes(const QuoteIn &in, int64_t M, int32_t k, int32_t 
 
 // The book as the loop sees it. GlobalBook: the market's arrays in global
 // memory. StagedBook: a copy of the market's records and level words (in LDS
-// on the GPU) that the loop reads and writes; it is copied back to global
-// memory when the market is done.
+// on the GPU) that the loop reads; its writes (order sizes, level words) go to
+// the copy and through to global memory, so global memory is current when the
+// walk ends and nothing is copied back (a walk changes a few words of a book of
+// 17 KB at the config-3 shape).
 struct GlobalBook {
   static constexpr bool kStaged = false;
   uint16_t *lv;
@@ -616,19 +618,26 @@ struct GlobalBook {
 
 struct StagedBook {
   static constexpr bool kStaged = true;
-  uint16_t *slv;
+  uint16_t *slv;  // the copy
   uint4 *srec;
+  uint16_t *glv;  // the market's arrays in global memory
+  uint4 *grec;
   ASTRA_HD uint4 record(uint32_t s) const { return srec[s]; }
   ASTRA_HD int32_t size(uint32_t s) const { return reinterpret_cast<const int32_t *>(srec + s)[0]; }
   ASTRA_HD uint32_t word(int32_t p, int side) const { return level_word(slv, p, side); }
   ASTRA_HD uint32_t head(int32_t p, int side) const { return level_head(slv, p, side); }
   ASTRA_HD void set_size(uint32_t s, int32_t v) const {
     reinterpret_cast<int32_t *>(srec + s)[0] = v;
+    gst(reinterpret_cast<int32_t *>(grec + s), v);
   }
   ASTRA_HD void set_word(int32_t p, int side, uint32_t w) const {
     store_level_word(slv, p, side, w);
+    gst(reinterpret_cast<uint32_t *>(glv + (size_t)p * 4 + 2 * side), w);
   }
-  ASTRA_HD void set_head(int32_t p, int side, uint32_t h) const { store_head(slv, p, side, h); }
+  ASTRA_HD void set_head(int32_t p, int side, uint32_t h) const {
+    store_head(slv, p, side, h);
+    gst(glv + (size_t)p * 4 + 2 * side, (uint16_t)h);
+  }
 };
 
 // Wave-uniform copies of the first active lane's values (readfirstlane; the
@@ -1507,6 +1516,8 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
       UniformStagedBook sb;
       sb.slv = reinterpret_cast<uint16_t *>(slv);
       sb.srec = srec;
+      sb.glv = reinterpret_cast<uint16_t *>(glv);
+      sb.grec = grec;
       RowBuffer rb{rows, kStageRows, 0, 0};
       if (lane == src) rb.base = sink.base;
       // The owning lane runs until its market is done or its row buffer is
@@ -1538,9 +1549,6 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
           rb.n = 0;
         }
       }
-      // the staged book back to global memory, coalesced
-      for (int32_t j = lane; j < b.O; j += 64) grec[j] = srec[j];
-      for (int32_t j = lane; j < b.L; j += 64) glv[j] = slv[j];
       if (lane == src) {
         sink.base = rb.base;
         quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, sb, ink.game, sok, &cy, last);
@@ -1675,7 +1683,7 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
       sink.flush(fo, c.pf, c.C);
       std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
       std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
-      const StagedBook sb{slv.data(), srec.data()};
+      const StagedBook sb{slv.data(), srec.data(), c.lv, c.rec};
       RowBuffer rb{rows.data(), kStageRows, 0, sink.base};
       bool fin = false;
       while (!fin) {
@@ -1685,8 +1693,6 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
         rb.base += rb.n;
         rb.n = 0;
       }
-      std::memcpy(c.rec, srec.data(), (size_t)h->O * 16);
-      std::memcpy(c.lv, slv.data(), (size_t)h->L * 8);
       sink.base = rb.base;
       if (b.stats) quote_epilogue<W, true, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok, cy, last);
       else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, sb, ink.game, sok, cy, last);
