@@ -117,6 +117,9 @@ struct astra_market {
   int32_t cus;                // CUs of the device
   int32_t per_wave;           // markets per wavefront of the matching kernel (0: default)
   int32_t fill_rows;          // fill rows a lane buffers before writing them (0: by grid)
+  int32_t helpers;            // market wavefronts per helper wavefront (0: no helpers)
+  int32_t hand_lanes;         // zero-size walks go to the helper when at most this many lanes loop
+  int32_t hand_queue;         // no hand-off while this many markets wait for the helper
   unsigned long long *stats;  // see astra_market_set_stats
   char *ws;
   size_t ws_bytes;
@@ -713,6 +716,181 @@ ASTRA_HD MarketCtx uniform_ctx(const MarketCtx &a) {
   return u;
 }
 
+// ---- hand-off of a market's loop to the workgroup's helper wavefront ----
+//
+// With helpers (quote_match_kernel's HELP > 0) each workgroup holds HELP
+// market wavefronts and one helper wavefront. A market lane whose walk is long
+// (a run of zero-size orders ahead, or many passes) packs its loop state at
+// the top of a pass into a slot of an LDS queue and leaves the market to the
+// helper, which finishes it from an LDS copy of the book while the market
+// wavefront goes on with its other lanes. Per market wavefront the queue has
+// kHandSlots slots of kSlotWords words, each with a flag word (0 free, 1
+// ready); then one done word per market wavefront.
+constexpr int kHandSlots = 4;
+constexpr int kSlotWords = 48;
+
+// Never hands off (every kernel without helpers, and the host build).
+struct NoHand {
+  static constexpr bool kOn = false;
+};
+
+// The loop state at the top of a pass and the call context of market c.m, as
+// words: what the helper needs to resume the loop and end the call.
+template <int W>
+ASTRA_HD void pack_slot(uint32_t *p, const LoopState<W> &s, const MarketCtx &c) {
+  static_assert(4 * W + 27 <= kSlotWords, "slot too small for the masks");
+  int i = 0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    p[i++] = (uint32_t)s.bm[w];
+    p[i++] = (uint32_t)(s.bm[w] >> 32);
+    p[i++] = (uint32_t)s.am[w];
+    p[i++] = (uint32_t)(s.am[w] >> 32);
+  }
+  p[i++] = (uint32_t)s.bb;
+  p[i++] = (uint32_t)s.ba;
+  p[i++] = s.bh;
+  p[i++] = s.ah;
+  p[i++] = s.brec.x;
+  p[i++] = s.brec.y;
+  p[i++] = s.brec.z;
+  p[i++] = s.brec.w;
+  p[i++] = s.arec.x;
+  p[i++] = s.arec.y;
+  p[i++] = s.arec.z;
+  p[i++] = s.arec.w;
+  p[i++] = (s.have_b ? 1u : 0u) | (s.have_a ? 2u : 0u) | (s.ahead ? 4u : 0u) |
+           (c.bid_ok ? 8u : 0u) | (c.ask_ok ? 16u : 0u) | (c.keep_b ? 32u : 0u) |
+           (c.keep_a ? 64u : 0u);
+  p[i++] = (uint32_t)s.pb;
+  p[i++] = (uint32_t)s.pa;
+  p[i++] = s.pbh;
+  p[i++] = s.pah;
+  p[i++] = (uint32_t)s.fc;
+  p[i++] = (uint32_t)s.last_px;
+  p[i++] = s.emptied;
+  p[i++] = s.forwarded;
+  p[i++] = s.npass;
+  p[i++] = s.zruns;
+  p[i++] = s.zrows;
+  p[i++] = (uint32_t)c.m;
+  p[i++] = (uint32_t)((uint64_t)c.m >> 32);
+  p[i++] = (uint32_t)c.ns;
+}
+
+// The inverse of pack_slot; the rest of the context follows from the book.
+template <int W>
+ASTRA_HD void unpack_slot(const uint32_t *p, const Book &b, LoopState<W> &s, MarketCtx &c) {
+  int i = 0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    s.bm[w] = (uint64_t)p[i] | ((uint64_t)p[i + 1] << 32);
+    s.am[w] = (uint64_t)p[i + 2] | ((uint64_t)p[i + 3] << 32);
+    i += 4;
+  }
+  s.bb = (int)p[i++];
+  s.ba = (int)p[i++];
+  s.bh = p[i++];
+  s.ah = p[i++];
+  s.brec = make_uint4(p[i], p[i + 1], p[i + 2], p[i + 3]);
+  i += 4;
+  s.arec = make_uint4(p[i], p[i + 1], p[i + 2], p[i + 3]);
+  i += 4;
+  const uint32_t f = p[i++];
+  s.have_b = (f & 1u) != 0;
+  s.have_a = (f & 2u) != 0;
+  s.ahead = (f & 4u) != 0;
+  c.bid_ok = (f & 8u) != 0;
+  c.ask_ok = (f & 16u) != 0;
+  c.keep_b = (f & 32u) != 0;
+  c.keep_a = (f & 64u) != 0;
+  s.pb = (int)p[i++];
+  s.pa = (int)p[i++];
+  s.pbh = p[i++];
+  s.pah = p[i++];
+  s.fc = (int32_t)p[i++];
+  s.last_px = (int32_t)p[i++];
+  s.emptied = p[i++];
+  s.forwarded = p[i++];
+  s.npass = p[i++];
+  s.zruns = p[i++];
+  s.zrows = p[i++];
+  c.m = (int64_t)((uint64_t)p[i] | ((uint64_t)p[i + 1] << 32));
+  i += 2;
+  c.ns = (int32_t)p[i++];
+  c.L = b.L;
+  c.O = b.O;
+  c.F = b.F;
+  c.C = b.C;
+  c.lv = b.levels + c.m * (int64_t)b.L * 4;
+  c.rec = b.records + c.m * (int64_t)b.O;
+  c.pf = b.portfolios + c.m * (int64_t)b.C * 2;
+  c.abort = false;
+}
+
+// A market wavefront's end of the queue.
+struct Hand {
+  static constexpr bool kOn = true;
+  uint32_t *slots;     // this wavefront's kHandSlots slots
+  uint32_t *flags;     // their flag words
+  uint32_t *queue;     // the flag words of every slot of the workgroup
+  int32_t queued;      // flag words in `queue`
+  int32_t max_queue;   // no hand-off while this many markets wait for the helper
+  int32_t threshold;   // passes after which any walk is handed off
+  int32_t zero_lanes;  // a zero-size walk is handed off when at most this many lanes loop
+  bool handed;         // this lane's market went to the helper
+};
+
+#if defined(__HIP_DEVICE_COMPILE__)
+// The value, hidden from the optimiser (it cannot fold branches on it).
+__device__ __forceinline__ bool opaque(bool v) {
+  int32_t x = v ? 1 : 0;
+  asm volatile("" : "+v"(x));
+  return x != 0;
+}
+
+// Called at the top of a pass by the lanes still in their loop (records loaded,
+// nothing of the pass done). Lanes that want to hand off take the free slots in
+// lane order; a lane that gets one writes its buffered rows, packs its state and
+// publishes the slot. Lanes left without a slot go on and ask again next pass.
+template <int W, class Sink>
+__device__ bool hand_off(Hand &h, bool want, const LoopState<W> &s, const MarketCtx &c, Sink &sink,
+                         const FillOut &out) {
+  const uint64_t req = __ballot(want);
+  if (req == 0) return false;
+  // markets already waiting for the helper: a long queue would keep this one
+  // waiting longer than its walk takes in global memory
+  int32_t waiting = 0;
+  for (int j = 0; j < h.queued; ++j)
+    waiting += (int32_t)__hip_atomic_load(h.queue + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  waiting = uni(waiting);
+  uint32_t freem = 0;
+#pragma unroll
+  for (int j = 0; j < kHandSlots; ++j)
+    freem |= (__hip_atomic_load(h.flags + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u
+                  ? 1u
+                  : 0u)
+             << j;
+  freem = uni(freem);
+  if (!want || freem == 0 || waiting >= h.max_queue) return false;
+  const int room = h.max_queue - waiting;
+  const int k = (int)__popcll(req & ((1ull << __lane_id()) - 1ull));
+  if (k >= __popc(freem) || k >= room) return false;
+  uint32_t f = freem;
+  for (int i = 0; i < k; ++i) f &= f - 1u;
+  const int j = __ffs(f) - 1;
+  // the helper read the slot before it freed it
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  sink.flush(out, c.pf, c.C);
+  pack_slot<W>(h.slots + j * kSlotWords, s, c);
+  // the book's writes, the rows and the slot before the flag
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __hip_atomic_store(h.flags + j, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  h.handed = true;
+  return true;
+}
+#endif
+
 // add_orders_kernel (market.cu:17-100) for market m and the set-up of the
 // matching loop (:122-142): masks, the inserts, the heads of the best levels
 // and their records.
@@ -983,9 +1161,12 @@ ASTRA_HD bool zero_walk(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, 
 // s and -s alternate). The reference loops until F fills and then writes -1;
 // here the owed rows are handed to the caller in `bulk`, the final state is set
 // directly, and the count is -1, which is the same result.
-template <int W, bool STATS, bool EARLY, class BookMem, class Sink>
+//
+// With a Hand (helpers), a lane whose walk is long hands its market off at the
+// top of a pass instead (returns false; hand->handed set).
+template <int W, bool STATS, bool EARLY, class BookMem, class Sink, class HandT = NoHand>
 ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, Sink &sink,
-                         const FillOut &out, Bulk &bulk, int32_t budget) {
+                         const FillOut &out, Bulk &bulk, int32_t budget, HandT *hand = nullptr) {
   const int32_t L = c.L, O = c.O, F = c.F;
   int32_t passes = 0;
   while (s.bb >= 0 && s.ba < L && s.bb >= s.ba) {
@@ -1033,7 +1214,18 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
       // such a run at instruction speed (0.2 us a row). Lanes that still have
       // company go on: the wavefront waits for them anyway. (At most 1, 2, 4,
       // 8 or any lane: 2 is fastest at 100,000 and 10,000 markets.)
-      if constexpr (EARLY) {
+      if constexpr (HandT::kOn) {
+#if defined(__HIP_DEVICE_COMPILE__)
+        const bool zstart = s.bh != s.ah && (((int32_t)s.brec.x == 0 && (int32_t)s.arec.x > 0) ||
+                                             ((int32_t)s.arec.x == 0 && (int32_t)s.brec.x > 0));
+        const bool want =
+            passes > hand->threshold || (zstart && lanes_here() <= hand->zero_lanes);
+        // (opaque: otherwise the compiler moves the slot's writes and its flag
+        // onto the loop's exit path, which runs only when every lane of the
+        // wavefront has left the loop, and the helper would see nothing before)
+        if (opaque(hand_off<W>(*hand, want, s, c, sink, out))) return false;
+#endif
+      } else if constexpr (EARLY) {
         const int32_t looping = lanes_here();
         if (budget != 0x7FFFFFFF && looping <= kEarlyStageLanes && s.bh != s.ah &&
             (((int32_t)s.brec.x == 0 && (int32_t)s.arec.x > 0) ||
@@ -1382,8 +1574,8 @@ typedef __attribute__((address_space(3))) void lvoid_t;  // LDS
 
 // Staged book of one market: records, level words (padded to 16 bytes), then
 // its row buffer.
-inline size_t stage_bytes(int32_t L, int32_t O) {
-  return (size_t)O * 16 + align_up((size_t)L * 8, 16) + (size_t)kStageRows * sizeof(uint4);
+ASTRA_HD size_t stage_bytes(int32_t L, int32_t O) {
+  return (size_t)O * 16 + ((size_t)L * 8 + 15) / 16 * 16 + (size_t)kStageRows * sizeof(uint4);
 }
 
 ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
@@ -1395,6 +1587,154 @@ ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
   (void)src;
   return v;
 #endif
+}
+
+// Finishes lane src's market from a copy of its book in LDS (`stage`: the
+// records, the level words padded to 16 bytes, then the row buffer). The whole
+// wavefront copies the book in with coalesced loads, the owning lane resumes
+// its loop reading the copy (on wave-uniform copies of its state), and all 64
+// lanes write the rows out, coalesced, each time the row buffer fills and at
+// the end; then the owning lane writes the call's epilogue. All 64 lanes call
+// this together.
+template <int W, bool STATS, bool GAME, bool MULTI, class Sink>
+__device__ void finish_staged(const Book &b, const FillOut &out, int32_t *stage, int lane, int src,
+                              int64_t m, MarketCtx &c, LoopState<W> &st, Sink &sink, Bulk &bulk,
+                              const GameMove &game, const StepOut &sok, Carry<W> *cy, bool last) {
+  const int64_t ms = shfl_i64(m, src);
+  uint4 *srec = reinterpret_cast<uint4 *>(stage);
+  uint64_t *slv = reinterpret_cast<uint64_t *>(srec + b.O);
+  uint4 *rows = reinterpret_cast<uint4 *>(slv + ((b.L + 1) & ~1));  // 16-byte aligned
+  uint4 *grec = b.records + ms * (int64_t)b.O;
+  uint64_t *glv = reinterpret_cast<uint64_t *>(b.levels) + ms * (int64_t)b.L;
+  int32_t *pfm = b.portfolios + ms * (int64_t)b.C * 2;
+  __builtin_amdgcn_wave_barrier();
+#if defined(__HIP_DEVICE_COMPILE__)
+  // LDS DMA (global_load_lds): each lane's 16 (or 4) bytes go straight to LDS
+  // at the wave-uniform base + lane * size, no registers involved, all loads
+  // in flight together.
+  for (int32_t j = 0; j < b.O; j += 64)
+    if (j + lane < b.O)
+      __builtin_amdgcn_global_load_lds((gvoid_t *)(grec + j + lane), (lvoid_t *)(srec + j), 16, 0,
+                                       0);
+  const uint32_t *glv32 = reinterpret_cast<const uint32_t *>(glv);
+  uint32_t *slv32 = reinterpret_cast<uint32_t *>(slv);
+  for (int32_t j = 0; j < 2 * b.L; j += 64)
+    if (j + lane < 2 * b.L)
+      __builtin_amdgcn_global_load_lds((gvoid_t *)(glv32 + j + lane), (lvoid_t *)(slv32 + j), 4, 0,
+                                       0);
+  __builtin_amdgcn_s_waitcnt(0);
+#endif
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  UniformStagedBook sb;
+  sb.slv = reinterpret_cast<uint16_t *>(slv);
+  sb.srec = srec;
+  sb.glv = reinterpret_cast<uint16_t *>(glv);
+  sb.grec = grec;
+  RowBuffer rb{rows, kStageRows, 0, 0};
+  if (lane == src) rb.base = sink.base;
+  // The owning lane runs until its market is done or its row buffer is full
+  // (on uniform copies of its state); then all 64 lanes write the rows out.
+  bool done = false;
+  while (!done) {
+    int32_t fin = 0;
+    if (lane == src) {
+      LoopState<W> us = uniform_state(st);
+      const MarketCtx uc = uniform_ctx(c);
+      RowBuffer urb{rows, kStageRows, uni(rb.n), uni(rb.base)};
+      fin = match_loop<W, STATS, false>(us, uc, sb, urb, out, bulk, 0x7FFFFFFF) ? 1 : 0;
+      st = us;
+      rb.n = urb.n;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int32_t n = __shfl(rb.n, src);
+    const int64_t base = shfl_i64(rb.base, src);
+    done = __shfl(fin, src) != 0;
+    flush_rows(out, rows, srec, n, base, pfm, b.C, lane, 64);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == src) {
+      rb.base += n;
+      rb.n = 0;
+    }
+  }
+  if (lane == src) {
+    sink.base = rb.base;
+    quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, sb, game, sok, cy, last);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Polls before a helper wavefront with nothing left to wait for gives up: far
+// beyond any market wavefront's lifetime (each poll sleeps about 0.1 us), it
+// only bounds the kernel if a market wavefront never signalled its end.
+constexpr int32_t kHelperMaxPolls = 1 << 22;
+
+// The helper wavefront of a workgroup with H market wavefronts: takes ready
+// slots of the queue in LDS (lowest first), frees each slot once its state is
+// read, finishes the market (finish_staged, lane 0 walking) and writes its
+// repeating rows; returns when every market wavefront has signalled its end and
+// no slot is ready.
+template <int W, int H>
+__device__ void helper_wave(const Book &b, const FillOut &out, int32_t *stage, uint32_t *slots,
+                            uint32_t *flags, const uint32_t *done, int lane) {
+  FillSink<4> sink;  // never buffers a row: the epilogue's flush finds it empty
+#if defined(__HIP_DEVICE_COMPILE__)
+  sink.lds = stage;
+  sink.lane = lane;
+#endif
+  int32_t polls = 0;
+  for (;;) {
+    uint32_t ready = 0;
+#pragma unroll
+    for (int j = 0; j < H * kHandSlots; ++j)
+      ready |= (__hip_atomic_load(flags + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 1u
+                    ? 1u
+                    : 0u)
+               << j;
+    ready = uni(ready);
+    if (ready) {
+      const int j = __ffs(ready) - 1;
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      LoopState<W> st;
+      MarketCtx c;
+      unpack_slot<W>(slots + j * kSlotWords, b, st, c);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0) __hip_atomic_store(flags + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      sink.n = 0;
+      sink.base = c.m * (int64_t)b.F + st.fc;
+      Bulk bulk;
+      bulk.count = 0;
+      finish_staged<W, false, false, false>(b, out, stage, lane, 0, c.m, c, st, sink, bulk,
+                                            GameMove{}, StepOut{}, (Carry<W> *)nullptr, true);
+      if (lane != 0) bulk.count = 0;
+      write_bulk_wave(out, bulk);
+      polls = 0;
+      continue;
+    }
+    uint32_t ended = 0;
+#pragma unroll
+    for (int i = 0; i < H; ++i)
+      ended += __hip_atomic_load(done + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (uni(ended) == (uint32_t)H) {
+      // every slot published before a done word is ready by now
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      uint32_t left = 0;
+#pragma unroll
+      for (int j = 0; j < H * kHandSlots; ++j)
+        left |= __hip_atomic_load(flags + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (uni(left) == 0u) return;
+      continue;
+    }
+    if (++polls > kHelperMaxPolls) return;
+    __builtin_amdgcn_s_sleep(2);
+  }
 }
 
 // Fused add + match + BBO, one lane per market, in two passes.
@@ -1415,13 +1755,24 @@ ASTRA_HD int64_t shfl_i64(int64_t v, int src) {
 // delay it. With FR = 4 the book reuses the row buffer's LDS (the whole grid of
 // a large launch fits on the CUs only that way), so the finished lanes write
 // their epilogues, rows included, before it.
-// All 64 lanes of a wavefront reach the ballots (no early return).
-template <int W, bool STATS, bool GAME, bool MULTI, bool ROWS, int FR>
+// HELP > 0 (large grids, FR = 4, single-step calls): each workgroup is HELP
+// market wavefronts and one helper wavefront, and step 2 runs on the helper
+// instead, concurrently with the market wavefronts' loops: a lane whose walk is
+// long (`budget` passes, or a run of zero-size orders ahead while at most
+// `hand_lanes` lanes of its wavefront still loop) hands its market over
+// through an LDS queue (hand_off, helper_wave) and its wavefront goes on. LDS
+// per workgroup: the HELP row buffers, the helper's staged book, the queue.
+// All 64 lanes of a wavefront reach the ballots (no early return but the
+// helper wavefront's, which returns as a whole).
+template <int W, bool STATS, bool GAME, bool MULTI, bool ROWS, int FR, int HELP = 0>
 __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, FillOut out,
                                                           StepOut so, int32_t steps,
                                                           int32_t budget, int32_t wave_words,
-                                                          int32_t per_wave) {
+                                                          int32_t per_wave, int32_t hand_lanes,
+                                                          int32_t hand_queue) {
   constexpr bool kApart = FR == 2;  // the staged book beside the row buffer
+  static_assert(HELP == 0 || (!STATS && !GAME && !MULTI && FR == 4 && W <= 4),
+                "helpers serve plain single-step calls of large grids");
   extern __shared__ int32_t lds_words[];
   // The FillBatch layout is a template argument: the other layout's pointers
   // become constant nulls, so their code and registers drop out.
@@ -1447,9 +1798,28 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
   // Lanes [0, per_wave) of each wavefront own one market each; the rest idle
   // (and help with the wavefront's cooperative copies).
   const int lane = (int)(threadIdx.x % 64);
-  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64;
+  const int wv = (int)uni((int32_t)(threadIdx.x / 64));  // wavefront within the workgroup
+  Hand hand{nullptr, nullptr, nullptr, 0, hand_queue, budget, hand_lanes, false};
+  if constexpr (HELP > 0) {
+    int32_t *stage = lds_words + HELP * wave_words;
+    uint32_t *slots = reinterpret_cast<uint32_t *>(stage + stage_bytes(b.L, b.O) / 4);
+    uint32_t *flags = slots + HELP * kHandSlots * kSlotWords;
+    uint32_t *done = flags + HELP * kHandSlots;
+    if (threadIdx.x < HELP * (kHandSlots + 1)) flags[threadIdx.x] = 0u;
+    __syncthreads();
+    if (wv == HELP) {
+      helper_wave<W, HELP>(b, out, stage, slots, flags, done, lane);
+      return;
+    }
+    hand.slots = slots + wv * kHandSlots * kSlotWords;
+    hand.flags = flags + wv * kHandSlots;
+    hand.queue = flags;
+    hand.queued = HELP * kHandSlots;
+  }
+  const int64_t wave = HELP > 0 ? (int64_t)blockIdx.x * HELP + wv
+                                : ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64;
   const int64_t m = lane < per_wave ? wave * per_wave + lane : b.M;
-  int32_t *wave_lds = lds_words + uni((int32_t)(threadIdx.x / 64) * wave_words);
+  int32_t *wave_lds = lds_words + wv * wave_words;
   FillSink<FR> sink;
 #if defined(__HIP_DEVICE_COMPILE__)
   sink.lds = wave_lds;
@@ -1472,7 +1842,11 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     if (m < b.M && !(GAME && c.abort)) {
       sink.base = m * (int64_t)b.F;
       const GlobalBook gb{c.lv, c.rec};
-      if (match_loop<W, STATS, !GAME>(st, c, gb, sink, out, bulk, budget)) {
+      if constexpr (HELP > 0) {
+        // the loop ends here or hands the market to the helper
+        if (match_loop<W, STATS, false>(st, c, gb, sink, out, bulk, 0x7FFFFFFF, &hand))
+          quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, gb, ink.game, sok, &cy, last);
+      } else if (match_loop<W, STATS, !GAME>(st, c, gb, sink, out, bulk, budget)) {
         if constexpr (kApart)
           finished = true;
         else
@@ -1482,80 +1856,12 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
         suspended = true;
       }
     }
-    uint64_t todo = __ballot(suspended);
+    uint64_t todo = HELP > 0 ? 0ull : __ballot(suspended);
     while (todo) {
       const int src = __ffsll((unsigned long long)todo) - 1;
       todo &= todo - 1;
-      const int64_t ms = shfl_i64(m, src);
-      uint4 *srec = reinterpret_cast<uint4 *>(wave_lds + (kApart ? sink_bytes(FR) / 4 : 0));
-      uint64_t *slv = reinterpret_cast<uint64_t *>(srec + b.O);
-      uint4 *rows = reinterpret_cast<uint4 *>(slv + ((b.L + 1) & ~1));  // 16-byte aligned
-      uint4 *grec = b.records + ms * (int64_t)b.O;
-      uint64_t *glv = reinterpret_cast<uint64_t *>(b.levels) + ms * (int64_t)b.L;
-      int32_t *pfm = b.portfolios + ms * (int64_t)b.C * 2;
-      __builtin_amdgcn_wave_barrier();
-#if defined(__HIP_DEVICE_COMPILE__)
-      // LDS DMA (global_load_lds): each lane's 16 (or 4) bytes go straight to
-      // LDS at the wave-uniform base + lane * size, no registers involved, all
-      // loads in flight together.
-      for (int32_t j = 0; j < b.O; j += 64)
-        if (j + lane < b.O)
-          __builtin_amdgcn_global_load_lds((gvoid_t *)(grec + j + lane), (lvoid_t *)(srec + j), 16,
-                                           0, 0);
-      const uint32_t *glv32 = reinterpret_cast<const uint32_t *>(glv);
-      uint32_t *slv32 = reinterpret_cast<uint32_t *>(slv);
-      for (int32_t j = 0; j < 2 * b.L; j += 64)
-        if (j + lane < 2 * b.L)
-          __builtin_amdgcn_global_load_lds((gvoid_t *)(glv32 + j + lane), (lvoid_t *)(slv32 + j), 4,
-                                           0, 0);
-      __builtin_amdgcn_s_waitcnt(0);
-#endif
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      UniformStagedBook sb;
-      sb.slv = reinterpret_cast<uint16_t *>(slv);
-      sb.srec = srec;
-      sb.glv = reinterpret_cast<uint16_t *>(glv);
-      sb.grec = grec;
-      RowBuffer rb{rows, kStageRows, 0, 0};
-      if (lane == src) rb.base = sink.base;
-      // The owning lane runs until its market is done or its row buffer is
-      // full (on uniform copies of its state); then all 64 lanes write the rows
-      // out, coalesced.
-      bool done = false;
-      while (!done) {
-        int32_t fin = 0;
-        if (lane == src) {
-          LoopState<W> us = uniform_state(st);
-          const MarketCtx uc = uniform_ctx(c);
-          RowBuffer urb{rows, kStageRows, uni(rb.n), uni(rb.base)};
-          fin = match_loop<W, STATS, false>(us, uc, sb, urb, out, bulk, 0x7FFFFFFF) ? 1 : 0;
-          st = us;
-          rb.n = urb.n;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int32_t n = __shfl(rb.n, src);
-        const int64_t base = shfl_i64(rb.base, src);
-        done = __shfl(fin, src) != 0;
-        flush_rows(out, rows, srec, n, base, pfm, b.C, lane, 64);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane == src) {
-          rb.base += n;
-          rb.n = 0;
-        }
-      }
-      if (lane == src) {
-        sink.base = rb.base;
-        quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, sb, ink.game, sok, &cy, last);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      finish_staged<W, STATS, GAME, MULTI>(b, out, wave_lds + (kApart ? sink_bytes(FR) / 4 : 0), lane,
+                                           src, m, c, st, sink, bulk, ink.game, sok, &cy, last);
     }
     if constexpr (kApart) {
       if (finished)
@@ -1563,6 +1869,11 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
                                               ink.game, sok, &cy, last);
     }
     write_bulk_wave(out, bulk);
+    if constexpr (HELP > 0) {  // this wavefront has handed off all it will
+      uint32_t *done = hand.flags - wv * kHandSlots + HELP * kHandSlots;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0) __hip_atomic_store(done + wv, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     if (MULTI) {  // this step's rows and book writes come before the next step's
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -1681,6 +1992,11 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
       else quote_epilogue<W, false, GAME, MULTI>(b, fo, c, st, sink, gb, ink.game, sok, cy, last);
     } else {  // the second pass, as on the GPU
       sink.flush(fo, c.pf, c.C);
+      if constexpr (!GAME && W <= 4) {  // through a queue slot, as a hand-off to a helper would
+        uint32_t slot[kSlotWords];
+        pack_slot<W>(slot, st, c);
+        unpack_slot<W>(slot, b, st, c);
+      }
       std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
       std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
       const StagedBook sb{slv.data(), srec.data(), c.lv, c.rec};
@@ -1711,6 +2027,40 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   }
 #else
   const size_t sink_b = sink_bytes(rows_cap);
+  // Helpers (single-step calls of plain large grids whose books stage): HELP
+  // market wavefronts and a helper per workgroup, if every workgroup the grid
+  // puts on a CU still fits in its LDS.
+  if constexpr (W <= 4 && !GAME && !MULTI) {
+    const int helpers = h->helpers;
+    if (helpers > 0 && staged && !b.stats && rows_cap == 4 && per_wave == 64) {
+      const size_t lds_h = (size_t)helpers * sink_b + stage_b +
+                           (size_t)helpers * (kHandSlots * (kSlotWords + 1) + 1) * 4;
+      const int64_t blocks = (waves + helpers - 1) / helpers;
+      const int64_t blocks_per_cu = (blocks + h->cus - 1) / h->cus;
+      if (lds_h <= (size_t)h->lds_limit && (size_t)blocks_per_cu * lds_h <= (size_t)h->lds_per_cu) {
+        const dim3 grid_h((unsigned)blocks), block_h((unsigned)(64 * (helpers + 1)));
+        const int32_t ww = (int32_t)(sink_b / 4);
+#define ASTRA_LAUNCH_HELP(H_)                                                                   \
+  do {                                                                                          \
+    if (fo.rows)                                                                                \
+      hipLaunchKernelGGL((quote_match_kernel<W, false, false, false, true, 4, H_>), grid_h,     \
+                         block_h, lds_h, s, b, in, fo, so, steps, budget, ww, per_wave,         \
+                         h->hand_lanes, h->hand_queue);                         \
+    else                                                                                        \
+      hipLaunchKernelGGL((quote_match_kernel<W, false, false, false, false, 4, H_>), grid_h,    \
+                         block_h, lds_h, s, b, in, fo, so, steps, budget, ww, per_wave,         \
+                         h->hand_lanes, h->hand_queue);                         \
+  } while (0)
+        if (helpers == 2)
+          ASTRA_LAUNCH_HELP(2);
+        else
+          ASTRA_LAUNCH_HELP(3);
+#undef ASTRA_LAUNCH_HELP
+        ASTRA_HIP_CHECK(rt_last_error(), "AddTwoSidedQuotes");
+        return ASTRA_OK;
+      }
+    }
+  }
   const size_t wave_bytes = rows_cap == 2 ? sink_b + stage_b : std::max(sink_b, stage_b);
   const size_t lds = (size_t)(h->block / 64) * wave_bytes;
   const int32_t wave_words = (int32_t)(wave_bytes / 4);
@@ -1720,27 +2070,27 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   if (b.stats && fo.rows)
     hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI, true, 4>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave);
+                       per_wave, 0, 0);
   else if (b.stats)
     hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI, false, 4>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave);
+                       per_wave, 0, 0);
   else if (fo.rows && rows_cap == 2 && !MULTI)
     hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, true, MULTI ? 4 : 2>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave);
+                       per_wave, 0, 0);
   else if (fo.rows)
     hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, true, 4>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave);
+                       per_wave, 0, 0);
   else if (rows_cap == 2 && !MULTI)
     hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, false, MULTI ? 4 : 2>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave);
+                       per_wave, 0, 0);
   else
     hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, false, 4>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave);
+                       per_wave, 0, 0);
 #endif
   ASTRA_HIP_CHECK(rt_last_error(), "AddTwoSidedQuotes");
   return ASTRA_OK;
@@ -1893,6 +2243,29 @@ int32_t default_fill_rows() {
   return (x == 2 || x == 4) ? x : 0;
 }
 
+// ASTRA_MARKET_HELPERS: market wavefronts per helper wavefront (2 or 3; 0 turns
+// helpers off). ASTRA_MARKET_HAND_LANES: a lane about to walk zero-size orders
+// hands its market to the helper when at most this many lanes of its wavefront
+// still loop (1-64).
+int32_t default_helpers() {
+  const char *e = std::getenv("ASTRA_MARKET_HELPERS");
+  const int x = e ? std::atoi(e) : 2;
+  return (x == 2 || x == 3) ? x : 0;
+}
+
+int32_t default_hand_lanes() {
+  const char *e = std::getenv("ASTRA_MARKET_HAND_LANES");
+  const int x = e ? std::atoi(e) : 64;
+  return (x >= 1 && x <= 64) ? x : 64;
+}
+
+// ASTRA_MARKET_HAND_QUEUE: markets that may wait for a helper at once (1-12).
+int32_t default_hand_queue() {
+  const char *e = std::getenv("ASTRA_MARKET_HAND_QUEUE");
+  const int x = e ? std::atoi(e) : 1;
+  return (x >= 1 && x <= 12) ? x : 1;
+}
+
 int default_block() {
   const char *e = std::getenv("ASTRA_MARKET_BLOCK");
   if (e) {
@@ -1975,6 +2348,9 @@ int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, i
   h->cus = cus > 0 ? cus : 1;
   h->per_wave = default_per_wave();
   h->fill_rows = default_fill_rows();
+  h->helpers = default_helpers();
+  h->hand_lanes = default_hand_lanes();
+  h->hand_queue = default_hand_queue();
   h->stats = nullptr;
   h->ws = static_cast<char *>(workspace);
   h->ws_bytes = workspace_bytes;

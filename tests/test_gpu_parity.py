@@ -71,6 +71,25 @@ def test_gpu_config3_subset_with_eviction(stage_budget, layout):
     assert r["fill_rows"] > 4000
 
 
+@pytest.mark.parametrize("helpers,hand_lanes,stage_budget,layout", [
+    (0, None, None, "columns"), (3, 64, None, "columns"), (3, 1, None, "columns"),
+    (2, 64, None, "rows"), (3, 64, 1, "columns"), (2, 2, 4, "rows")])
+def test_gpu_config3_subset_helpers(helpers, hand_lanes, stage_budget, layout):
+    """Config 3 markets 0..3999 for all 1000 steps with 4 fill rows per lane, the
+    launch shape of a large grid: markets whose walks are long go to the helper
+    wavefront of their workgroup (helpers 2 or 3) or, without helpers, are
+    finished by their own wavefront after its loop. hand_lanes 64 hands off
+    every zero-size walk, 1 only a lane left alone; stage budget 1 hands off
+    every market that crosses twice."""
+    cfg, gen = _stream_gen(3, np.arange(4000))
+    _log(f"config 3 subset with helpers {helpers}, hand lanes {hand_lanes}, budget {stage_budget}, "
+         f"{layout}")
+    r = run_parity(4000, cfg.L, cfg.O, cfg.F, cfg.C, 1000, gen, bbo_every=1, full_every=250,
+                   label="cfg3 helpers", stage_budget=stage_budget, layout=layout, fill_rows=4,
+                   helpers=helpers, hand_lanes=hand_lanes)
+    assert r["fill_rows"] > 4000
+
+
 def test_gpu_config4_subset_deep_book():
     """Config 4 shape (L=512: 8 mask words, O=F=4096, C=64) on 300 markets x 2000 steps."""
     cfg, gen = _stream_gen(4, np.arange(300))
@@ -96,11 +115,13 @@ ALIAS_CASES = [
 ]
 
 
-@pytest.mark.parametrize("stage_budget,layout,fill_rows", [(None, "columns", None), (1, "columns", None),
-                                                           (1, "rows", None), (1, "columns", 4)])
+@pytest.mark.parametrize("stage_budget,layout,fill_rows,helpers", [
+    (None, "columns", None, None), (1, "columns", None, None), (1, "rows", None, None),
+    (1, "columns", 4, 0), (1, "columns", 4, 3), (None, "rows", 4, 2)])
 @pytest.mark.parametrize("M,L,O,F,C,steps,seed", ALIAS_CASES)
-def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, layout, fill_rows):
-    _log(f"aliasing M={M} L={L} O={O} F={F} stage budget {stage_budget} {layout} fill rows {fill_rows}")
+def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, layout, fill_rows, helpers):
+    _log(f"aliasing M={M} L={L} O={O} F={F} stage budget {stage_budget} {layout} fill rows {fill_rows} "
+         f"helpers {helpers}")
     rng = np.random.default_rng(seed)
     hot = max(4, min(L, 24))  # concentrate prices so books cross often
 
@@ -114,7 +135,7 @@ def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, lay
                 rng.integers(-1, 8, M).astype(np.int32), rng.integers(-1, C + 2, M).astype(np.int32))
 
     r = run_parity(M, L, O, F, C, steps, gen, full_every=50, label=f"alias L{L} O{O}",
-                   stage_budget=stage_budget, layout=layout, fill_rows=fill_rows)
+                   stage_budget=stage_budget, layout=layout, fill_rows=fill_rows, helpers=helpers)
     if O <= 3:
         assert r["overflows"] > 0
 
