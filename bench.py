@@ -616,18 +616,19 @@ def profile_traffic(prefix: str, kernel: str, window):
     starts with `prefix` (copy-calibrated), or (None, None) when no summary holds a
     figure for exactly that window (traffic depends on the book's state, so a
     figure from other steps would describe other work). `kernel` is the name up to
-    its closing '>'; the matching kernel's last template argument, the fill rows a
-    lane buffers (2 or 4), is the engine's choice for the grid and may follow."""
+    its closing '>'; the matching kernel's last two template arguments, the fill rows
+    a lane buffers (2 or 4) and the market wavefronts per helper wavefront (0, 2 or
+    3), are the engine's choice for the grid and may follow."""
     import glob
     import re
-    key = re.compile(r"traffic_bytes_per_launch\[void " + re.escape(kernel) + r"(, [24])?>\]\["
+    key = re.compile(r"traffic_bytes_per_launch\[void " + re.escape(kernel) + r"(, [24](, [0-3])?)?>\]\["
                      + f"{window[0]},{window[1]}" + r"\]:\s*(\S+)")
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", prefix + "*.md"))):
         with open(path) as f:
             for line in f:
                 m = key.match(line)
                 if m:
-                    return float(m.group(2)), os.path.relpath(path, ROOT)
+                    return float(m.group(3)), os.path.relpath(path, ROOT)
     return None, None
 
 
