@@ -1954,10 +1954,20 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
                       (size_t)(h->block / 64) * align_up(stage_bytes(h->L, h->O), 16) <=
                           (size_t)h->lds_limit;
   const int32_t budget = staged ? h->stage_budget : 0x7FFFFFFF;
-  const int32_t per_wave = markets_per_wave(h, GAME);
+  const size_t stage_b = staged ? align_up(stage_bytes(h->L, h->O), 16) : (size_t)0;
+  int32_t per_wave = markets_per_wave(h, GAME);
+  // A single-step grid of at most one full wavefront per CU leaves most SIMDs
+  // idle: half-full wavefronts end sooner (each waits for the slowest of fewer
+  // markets), where the doubled grid still fits on the CUs at once with the
+  // small grids' LDS per wavefront (config 2, 10,000 markets: +4%; at config 4
+  // the doubled grid would not fit and run in two rounds).
+  if (!h->per_wave && !GAME && !MULTI && (int64_t)b.M <= (int64_t)64 * h->cus) {
+    const size_t wb = sink_bytes(2) + stage_b;
+    const int64_t resident = (int64_t)h->cus * (int64_t)((size_t)h->lds_per_cu / wb);
+    if (2 * (((int64_t)b.M + 63) / 64) <= resident) per_wave = 32;
+  }
   const int64_t waves = ((int64_t)b.M + per_wave - 1) / per_wave;
   const int64_t waves_per_cu = (waves + h->cus - 1) / h->cus;
-  const size_t stage_b = staged ? align_up(stage_bytes(h->L, h->O), 16) : (size_t)0;
   // (a multi-step launch buffers 4: its wavefronts go on to the next step; and 2
   // only where the staged book fits beside the row buffer for every wavefront
   // the grid puts on a CU)
