@@ -833,9 +833,11 @@ struct Hand {
   static constexpr bool kOn = true;
   uint32_t *slots;     // this wavefront's kHandSlots slots
   uint32_t *flags;     // their flag words
-  uint32_t *queue;     // the flag words of every slot of the workgroup
+  uint32_t *queue;     // the flag words of every slot of the workgroup, then the
+                       // helper's busy word
   int32_t queued;      // flag words in `queue`
-  int32_t max_queue;   // no hand-off while this many markets wait for the helper
+  int32_t max_queue;   // no hand-off while this many markets wait for the helper or
+                       // are being finished by it
   int32_t threshold;   // passes after which any walk is handed off
   int32_t zero_lanes;  // a zero-size walk is handed off when at most this many lanes loop
   bool handed;         // this lane's market went to the helper
@@ -858,10 +860,11 @@ __device__ bool hand_off(Hand &h, bool want, const LoopState<W> &s, const Market
                          const FillOut &out) {
   const uint64_t req = __ballot(want);
   if (req == 0) return false;
-  // markets already waiting for the helper: a long queue would keep this one
-  // waiting longer than its walk takes in global memory
+  // markets already with the helper (waiting, or the one it is finishing): a
+  // long queue would keep this one waiting longer than its walk takes in
+  // global memory
   int32_t waiting = 0;
-  for (int j = 0; j < h.queued; ++j)
+  for (int j = 0; j <= h.queued; ++j)
     waiting += (int32_t)__hip_atomic_load(h.queue + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   waiting = uni(waiting);
   uint32_t freem = 0;
@@ -1684,6 +1687,7 @@ constexpr int32_t kHelperMaxPolls = 1 << 22;
 template <int W, int H>
 __device__ void helper_wave(const Book &b, const FillOut &out, int32_t *stage, uint32_t *slots,
                             uint32_t *flags, const uint32_t *done, int lane) {
+  uint32_t *busy = flags + H * kHandSlots;  // 1 while a market is being finished
   FillSink<4> sink;  // never buffers a row: the epilogue's flush finds it empty
 #if defined(__HIP_DEVICE_COMPILE__)
   sink.lds = stage;
@@ -1706,7 +1710,10 @@ __device__ void helper_wave(const Book &b, const FillOut &out, int32_t *stage, u
       MarketCtx c;
       unpack_slot<W>(slots + j * kSlotWords, b, st, c);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      if (lane == 0) __hip_atomic_store(flags + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (lane == 0) {
+        __hip_atomic_store(busy, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_store(flags + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
       sink.n = 0;
       sink.base = c.m * (int64_t)b.F + st.fc;
       Bulk bulk;
@@ -1715,6 +1722,7 @@ __device__ void helper_wave(const Book &b, const FillOut &out, int32_t *stage, u
                                             GameMove{}, StepOut{}, (Carry<W> *)nullptr, true);
       if (lane != 0) bulk.count = 0;
       write_bulk_wave(out, bulk);
+      if (lane == 0) __hip_atomic_store(busy, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       polls = 0;
       continue;
     }
@@ -1804,8 +1812,8 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     int32_t *stage = lds_words + HELP * wave_words;
     uint32_t *slots = reinterpret_cast<uint32_t *>(stage + stage_bytes(b.L, b.O) / 4);
     uint32_t *flags = slots + HELP * kHandSlots * kSlotWords;
-    uint32_t *done = flags + HELP * kHandSlots;
-    if (threadIdx.x < HELP * (kHandSlots + 1)) flags[threadIdx.x] = 0u;
+    uint32_t *done = flags + HELP * kHandSlots + 1;  // after the helper's busy word
+    if (threadIdx.x < HELP * (kHandSlots + 1) + 1) flags[threadIdx.x] = 0u;
     __syncthreads();
     if (wv == HELP) {
       helper_wave<W, HELP>(b, out, stage, slots, flags, done, lane);
@@ -1870,7 +1878,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     }
     write_bulk_wave(out, bulk);
     if constexpr (HELP > 0) {  // this wavefront has handed off all it will
-      uint32_t *done = hand.flags - wv * kHandSlots + HELP * kHandSlots;
+      uint32_t *done = hand.flags - wv * kHandSlots + HELP * kHandSlots + 1;
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0) __hip_atomic_store(done + wv, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
@@ -2044,7 +2052,7 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
     const int helpers = h->helpers;
     if (helpers > 0 && staged && !b.stats && rows_cap == 4 && per_wave == 64) {
       const size_t lds_h = (size_t)helpers * sink_b + stage_b +
-                           (size_t)helpers * (kHandSlots * (kSlotWords + 1) + 1) * 4;
+                           ((size_t)helpers * (kHandSlots * (kSlotWords + 1) + 1) + 1) * 4;
       const int64_t blocks = (waves + helpers - 1) / helpers;
       const int64_t blocks_per_cu = (blocks + h->cus - 1) / h->cus;
       if (lds_h <= (size_t)h->lds_limit && (size_t)blocks_per_cu * lds_h <= (size_t)h->lds_per_cu) {
@@ -2269,11 +2277,12 @@ int32_t default_hand_lanes() {
   return (x >= 1 && x <= 64) ? x : 64;
 }
 
-// ASTRA_MARKET_HAND_QUEUE: markets that may wait for a helper at once (1-12).
+// ASTRA_MARKET_HAND_QUEUE: markets a helper may hold at once, the one it is
+// finishing included (1-13).
 int32_t default_hand_queue() {
   const char *e = std::getenv("ASTRA_MARKET_HAND_QUEUE");
-  const int x = e ? std::atoi(e) : 1;
-  return (x >= 1 && x <= 12) ? x : 1;
+  const int x = e ? std::atoi(e) : 2;
+  return (x >= 1 && x <= 13) ? x : 2;
 }
 
 int default_block() {
