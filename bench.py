@@ -319,7 +319,10 @@ def main():
         "work_per_step": {"inserts": n_ins / K, "fill_rows": n_fill / K, "levels_emptied": n_empty / K,
                           "overflow_markets": n_ovf / K, "crossing_markets": n_cross / K,
                           "loop_passes": n_pass / K, "staged_markets": n_staged / K,
-                          "staged_zero_runs": n_zruns / K, "staged_zero_rows": n_zrows / K},
+                          "staged_zero_runs": n_zruns / K, "staged_zero_rows": n_zrows / K,
+                          "staged_counts_note": "staged_* come from the counting kernel, which "
+                                                "stages serially (no helper wavefronts); the other "
+                                                "counts are the work of any launch shape"},
         "roofline": {
             "kernel": "quote_match_kernel",
             "bound": "hbm",
