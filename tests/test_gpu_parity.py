@@ -71,22 +71,25 @@ def test_gpu_config3_subset_with_eviction(stage_budget, layout):
     assert r["fill_rows"] > 4000
 
 
-@pytest.mark.parametrize("helpers,hand_lanes,stage_budget,layout", [
-    (0, None, None, "columns"), (3, 64, None, "columns"), (3, 1, None, "columns"),
-    (2, 64, None, "rows"), (3, 64, 1, "columns"), (2, 2, 4, "rows")])
-def test_gpu_config3_subset_helpers(helpers, hand_lanes, stage_budget, layout):
+@pytest.mark.parametrize("helpers,hand_lanes,stage_budget,layout,hand_queue", [
+    (0, None, None, "columns", None), (3, 64, None, "columns", None), (3, 1, None, "columns", None),
+    (2, 64, None, "rows", None), (3, 64, 1, "columns", None), (2, 2, 4, "rows", None),
+    (2, 64, 1, "columns", 13), (3, 64, None, "columns", 1)])
+def test_gpu_config3_subset_helpers(helpers, hand_lanes, stage_budget, layout, hand_queue):
     """Config 3 markets 0..3999 for all 1000 steps with 4 fill rows per lane, the
     launch shape of a large grid: markets whose walks are long go to the helper
     wavefront of their workgroup (helpers 2 or 3) or, without helpers, are
     finished by their own wavefront after its loop. hand_lanes 64 hands off
     every zero-size walk, 1 only a lane left alone; stage budget 1 hands off
-    every market that crosses twice."""
+    every market that crosses twice; hand_queue 13 lets every slot of a
+    workgroup fill (lanes then find no free slot and go on in global memory), 1
+    hands off only to an idle helper."""
     cfg, gen = _stream_gen(3, np.arange(4000))
     _log(f"config 3 subset with helpers {helpers}, hand lanes {hand_lanes}, budget {stage_budget}, "
-         f"{layout}")
+         f"{layout}, hand queue {hand_queue}")
     r = run_parity(4000, cfg.L, cfg.O, cfg.F, cfg.C, 1000, gen, bbo_every=1, full_every=250,
                    label="cfg3 helpers", stage_budget=stage_budget, layout=layout, fill_rows=4,
-                   helpers=helpers, hand_lanes=hand_lanes)
+                   helpers=helpers, hand_lanes=hand_lanes, hand_queue=hand_queue)
     assert r["fill_rows"] > 4000
 
 
@@ -117,7 +120,7 @@ ALIAS_CASES = [
 
 @pytest.mark.parametrize("stage_budget,layout,fill_rows,helpers", [
     (None, "columns", None, None), (1, "columns", None, None), (1, "rows", None, None),
-    (1, "columns", 4, 0), (1, "columns", 4, 3), (None, "rows", 4, 2)])
+    (1, "columns", 4, 0), (1, "columns", 4, 3), (None, "rows", 4, 2), (1, "rows", 4, 2)])
 @pytest.mark.parametrize("M,L,O,F,C,steps,seed", ALIAS_CASES)
 def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, layout, fill_rows, helpers):
     _log(f"aliasing M={M} L={L} O={O} F={F} stage budget {stage_budget} {layout} fill rows {fill_rows} "
