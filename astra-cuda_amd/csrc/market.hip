@@ -451,6 +451,8 @@ struct FillSink {
       if (R == 4 && (a & 15) == 0) {  // rows k..k+3 of a 4-row-aligned run
         if (n == 4) {
           gst(reinterpret_cast<int4 *>(d), make_int4(at(f, 0), at(f, 1), at(f, 2), at(f, 3)));
+        } else if (n == 3) {  // one 12-byte store instead of an 8- and a 4-byte one
+          gst(reinterpret_cast<int3 *>(d), make_int3(at(f, 0), at(f, 1), at(f, 2)));
         } else {
           if (n & 2) gst(reinterpret_cast<int2 *>(d), make_int2(at(f, 0), at(f, 1)));
           if (n & 1) gst(d + (n - 1), at(f, n - 1));
