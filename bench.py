@@ -80,6 +80,9 @@ def parse_args():
     ap.add_argument("--phases", default="ABCDRS",
                     help="phases to run (A is always run; B latency, C events, D work counts, "
                          "R row layout, S multi-step)")
+    ap.add_argument("--scatter-calibration", action="store_true",
+                    help="only time scattered 4-byte writes, reads and atomic adds into a 1 GiB "
+                         "buffer (the rate of scattered memory requests the device sustains)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for rocprof counter scaling)")
     return ap.parse_args()
@@ -113,6 +116,36 @@ def pre_roll(args, run_steps: int) -> int:
     return max(0, run_steps - args.warmup - args.steps)
 
 
+def scatter_calibration():
+    """Requests per second of scattered 4-byte accesses: 16M random offsets into a 1 GiB
+    int32 buffer, written (index_put_), read (gather) and atomically added (index_add_),
+    each timed with HIP events over 10 launches. Each access is one L1-to-L2 request
+    (offsets are random, so no two accesses of a wavefront share a line)."""
+    import torch
+    n, k = 1 << 28, 1 << 24
+    buf = torch.zeros(n, dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    idx = torch.randint(0, n, (k,), dtype=torch.int64, device="cuda", generator=g)
+    val = torch.ones(k, dtype=torch.int32, device="cuda")
+    out = {}
+    for name, fn in (("write", lambda: buf.index_put_((idx,), val)),
+                     ("read", lambda: torch.take(buf, idx)),
+                     ("atomic_add", lambda: buf.index_add_(0, idx, val))):
+        for _ in range(3):
+            fn()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(10):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        t = ev[0].elapsed_time(ev[1]) / 10 * 1e-3
+        out[name] = {"us_per_launch": t * 1e6, "requests_per_s": k / t}
+    print(json.dumps({"scatter_calibration": {"accesses_per_launch": k, "buffer_bytes": 4 * n, **out}}))
+
+
 def copy_calibration():
     import torch
     n = 1 << 30  # 1 GiB
@@ -133,6 +166,8 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         return copy_calibration()
+    if args.scatter_calibration:
+        return scatter_calibration()
 
     if args.config == 5:
         return bench_game(args)
@@ -288,6 +323,21 @@ def main():
     achieved = qm_bytes / qm_avg_s / 1e9
 
     traffic, traffic_src = measured_traffic(cfg, M, bbo, (T0, T))
+    requests = None
+    if M == cfg.M and bbo == cfg.bbo_every_step:
+        words = 1
+        while words * 64 < cfg.L:
+            words *= 2
+        found = profile_requests(f"quote_match_kernel<{words}, false, false, false, false", (T0, T))
+        if found:
+            req, rates, src = found
+            requests = {
+                "per_launch": req,
+                "per_s": sum(req.values()) / qm_avg_s,
+                "device_scatter_rates_per_s": rates,
+                "write_requests_at_device_rate_us": req["write"] / rates["write"] * 1e6,
+                "source": src,
+            }
     value = M * K / wall
     result = {
         "metric": "quote-matches/sec and market-steps/sec at 100k markets; p50 step latency",
@@ -334,6 +384,7 @@ def main():
             "traffic_source": traffic_src,
             "algorithmic_bytes_per_launch": qm_bytes,
             "get_bbos_algorithmic_bytes_per_launch": bbo_bytes,
+            "scattered_requests": requests,
         },
     }
 
@@ -633,6 +684,30 @@ def profile_traffic(prefix: str, kernel: str, window):
                 if m:
                     return float(m.group(3)), os.path.relpath(path, ROOT)
     return None, None
+
+
+def profile_requests(kernel: str, window):
+    """The matching kernel's scattered L1-to-L2 requests per launch (read, write, atomic)
+    over steps [window) and the device's scattered-request rates per second (the
+    scatter calibration), from a committed summary under profiles/, or None."""
+    import glob
+    import re
+    key = re.compile(r"requests_per_launch\[void " + re.escape(kernel) + r"(, [24](, [0-3])?)?>\]\["
+                     + f"{window[0]},{window[1]}" + r"\]: read (\S+) write (\S+) atomic (\S+)")
+    cal = re.compile(r"scatter_calibration_requests_per_s: read (\S+) write (\S+) atomic (\S+)")
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_request_rate.md"))):
+        req = rates = None
+        with open(path) as f:
+            for line in f:
+                m = key.match(line)
+                if m:
+                    req = {k: float(m.group(i)) for k, i in (("read", 3), ("write", 4), ("atomic", 5))}
+                c = cal.match(line)
+                if c:
+                    rates = {k: float(c.group(i)) for k, i in (("read", 1), ("write", 2), ("atomic", 3))}
+        if req and rates:
+            return req, rates, os.path.relpath(path, ROOT)
+    return None
 
 
 def measured_traffic(cfg, M, bbo, window):

@@ -167,6 +167,8 @@ def main():
     p.add_argument("dir")
     p.add_argument("--skip", type=int, default=100)
     p.add_argument("--take", type=int, default=900)
+    p.add_argument("--min-dispatches", type=int, default=100,
+                   help="skip kernels launched fewer times (set-up fills)")
     r = sub.add_parser("traffic")
     for n in ("fetch", "write", "copy_fetch", "copy_write"):
         r.add_argument(n)
@@ -178,7 +180,7 @@ def main():
     if a.cmd == "trace":
         print(trace(a.dir, [int(x) for x in a.blocks.split(",")], a.idle))
     elif a.cmd == "pmc":
-        print(pmc(a.dir, a.skip, a.take))
+        print(pmc(a.dir, a.skip, a.take, a.min_dispatches))
     else:
         print(traffic(a.fetch, a.write, a.copy_fetch, a.copy_write, a.skip, a.take, a.min_dispatches))
 

@@ -71,3 +71,16 @@ def test_profile_summary_idle_counts_only_time_no_kernel_ran():
     # overlapping spans are counted once
     disp = {"a": [(0, 100), (50, 100)], "b": [(120, 10)]}
     assert "no kernel ran 0.00 us" in ps.idle(disp, "a", 0, 2)
+
+
+def test_matching_kernel_requests_are_found_for_config3_driver_window():
+    """The scattered-request counts and the device's scatter rates of the committed
+    request-rate summary, for exactly the driver's window."""
+    cfg = CONFIGS[3]
+    found = bench.profile_requests("quote_match_kernel<2, false, false, false, false", _window(cfg.steps))
+    assert found is not None
+    req, rates, src = found
+    assert src.startswith("profiles/quote_match_config3_stress_100k_")
+    assert set(req) == set(rates) == {"read", "write", "atomic"}
+    assert all(v > 0 for v in req.values()) and all(v > 0 for v in rates.values())
+    assert bench.profile_requests("quote_match_kernel<2, false, false, false, false", (100, 1000)) is None
