@@ -76,8 +76,10 @@ def test_gpu_config3_subset_with_eviction(stage_budget, layout):
     (2, 64, None, "rows", None), (3, 64, 1, "columns", None), (2, 2, 4, "rows", None),
     (2, 64, 1, "columns", 13), (3, 64, None, "columns", 1)])
 def test_gpu_config3_subset_helpers(helpers, hand_lanes, stage_budget, layout, hand_queue):
-    """Config 3 markets 0..3999 for all 1000 steps with 4 fill rows per lane, the
-    launch shape of a large grid: markets whose walks are long go to the helper
+    """Config 3 markets 0..3999 for all 1000 steps with 4 fill rows per lane and 64
+    markets per wavefront, the launch shape of a large grid (a grid this small
+    would otherwise run 32 per wavefront, without helpers): markets whose walks are
+    long go to the helper
     wavefront of their workgroup (helpers 2 or 3) or, without helpers, are
     finished by their own wavefront after its loop. hand_lanes 64 hands off
     every zero-size walk, 1 only a lane left alone; stage budget 1 hands off
@@ -89,16 +91,22 @@ def test_gpu_config3_subset_helpers(helpers, hand_lanes, stage_budget, layout, h
          f"{layout}, hand queue {hand_queue}")
     r = run_parity(4000, cfg.L, cfg.O, cfg.F, cfg.C, 1000, gen, bbo_every=1, full_every=250,
                    label="cfg3 helpers", stage_budget=stage_budget, layout=layout, fill_rows=4,
-                   helpers=helpers, hand_lanes=hand_lanes, hand_queue=hand_queue)
+                   helpers=helpers, hand_lanes=hand_lanes, hand_queue=hand_queue, per_wave=64)
     assert r["fill_rows"] > 4000
 
 
-def test_gpu_config4_subset_deep_book():
-    """Config 4 shape (L=512: 8 mask words, O=F=4096, C=64) on 300 markets x 2000 steps."""
+@pytest.mark.parametrize("fill_rows,per_wave,stage_budget", [
+    (None, None, None), (4, 64, None), (4, 64, 1)])
+def test_gpu_config4_subset_deep_book(fill_rows, per_wave, stage_budget):
+    """Config 4 shape (L=512: 8 mask words, O=F=4096, C=64) on 300 markets x 2000 steps;
+    also with 4 fill rows per lane and 64 markets per wavefront, the launch of a large
+    grid, where a staged book of 4096 orders reuses its wavefront's row buffer in LDS
+    (stage budget 1: every market that crosses twice)."""
     cfg, gen = _stream_gen(4, np.arange(300))
-    _log("config 4 subset: 300 x 2000")
+    _log(f"config 4 subset: 300 x 2000, fill rows {fill_rows}, per wave {per_wave}, "
+         f"stage budget {stage_budget}")
     r = run_parity(300, cfg.L, cfg.O, cfg.F, cfg.C, 2000, gen, bbo_every=5, full_every=500,
-                   label="cfg4")
+                   label="cfg4", fill_rows=fill_rows, per_wave=per_wave, stage_budget=stage_budget)
     assert r["fill_rows"] > 300
 
 
@@ -138,7 +146,8 @@ def test_gpu_aliasing_and_overflow(M, L, O, F, C, steps, seed, stage_budget, lay
                 rng.integers(-1, 8, M).astype(np.int32), rng.integers(-1, C + 2, M).astype(np.int32))
 
     r = run_parity(M, L, O, F, C, steps, gen, full_every=50, label=f"alias L{L} O{O}",
-                   stage_budget=stage_budget, layout=layout, fill_rows=fill_rows, helpers=helpers)
+                   stage_budget=stage_budget, layout=layout, fill_rows=fill_rows, helpers=helpers,
+                   per_wave=None if helpers is None else 64)
     if O <= 3:
         assert r["overflows"] > 0
 
