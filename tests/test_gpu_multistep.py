@@ -18,10 +18,10 @@ pytestmark = pytest.mark.gpu
 BBO = ("best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes")
 
 
-def _run(M, L, O, F, C, stream, warm, chunks, layout, stage_budget=None, oracle=False):
+def _run(M, L, O, F, C, stream, warm, chunks, layout, stage_budget=None, oracle=False, **knobs):
     print(f"multistep M={M} L={L} O={O} F={F} C={C} warm={warm} chunks={chunks} layout={layout} "
-          f"budget={stage_budget}", flush=True)
-    single = make_market(M, L, O, F, C, stage_budget=stage_budget)
+          f"budget={stage_budget} {knobs}", flush=True)
+    single = make_market(M, L, O, F, C, stage_budget=stage_budget, **knobs)
     fs = single.new_fill_batch(layout)
     bs = single.new_bbo_batch()
     om = OracleMarket(M, L, O, F, C) if oracle else None
@@ -77,8 +77,12 @@ def _run(M, L, O, F, C, stream, warm, chunks, layout, stage_budget=None, oracle=
         assert torch.equal(getattr(bm, f), getattr(bs, f)), f
 
 
-@pytest.mark.parametrize("stage_budget,layout", [(None, "columns"), (1, "rows"), (0, "columns")])
-def test_gpu_multistep_aliasing_vs_oracle(stage_budget, layout):
+# per_wave: markets per wavefront (7 and 32 leave lanes of each wavefront idle through
+# every step, and 7 splits the markets over 46 wavefronts).
+@pytest.mark.parametrize("stage_budget,layout,knobs", [
+    (None, "columns", {}), (1, "rows", {}), (0, "columns", {}),
+    (1, "columns", {"per_wave": 32}), (1, "rows", {"per_wave": 7})])
+def test_gpu_multistep_aliasing_vs_oracle(stage_budget, layout, knobs):
     M, L, O, F, C = 320, 16, 3, 2, 4
     rng = np.random.default_rng(11)
 
@@ -98,7 +102,7 @@ def test_gpu_multistep_aliasing_vs_oracle(stage_budget, layout):
             cache[t] = gen(t)
         return cache[t]
 
-    _run(M, L, O, F, C, stream, 5, [1, 9, 0, 40, 64], layout, stage_budget, oracle=True)
+    _run(M, L, O, F, C, stream, 5, [1, 9, 0, 40, 64], layout, stage_budget, oracle=True, **knobs)
 
 
 @pytest.mark.parametrize("idx,M,warm,chunks,layout", [
