@@ -1,5 +1,7 @@
 """The high-low trading game on the HIP engine (astra_cuda.load_game) against the
 game oracle, bit-exact (GPU)."""
+import contextlib
+
 import numpy as np
 import pytest
 import torch
@@ -15,21 +17,35 @@ def _t(a):
     return torch.as_tensor(np.ascontiguousarray(a)).to(DEV)
 
 
-def _game(params, stage_budget=None):
+@contextlib.contextmanager
+def _engine_knobs(stage_budget=None, per_wave=None, fill_rows=None):
+    """Engine knobs for the markets created inside the block (a game creates its market
+    with each new state): the loop passes before a book is staged in LDS, envs per
+    wavefront of the fused move and fill rows a lane buffers (64 and 4 is the launch
+    of a large game, such as the reference benchmark's 262,144 envs)."""
     import os
+    env = {"ASTRA_MARKET_STAGE_BUDGET": stage_budget, "ASTRA_MARKET_PER_WAVE": per_wave,
+           "ASTRA_MARKET_FILL_ROWS": fill_rows}
+    old = {k: os.environ.get(k) for k in env}
+    for k, v in env.items():
+        if v is not None:
+            os.environ[k] = str(v)
+    try:
+        yield
+    finally:
+        for k, v in env.items():
+            if v is None:
+                continue
+            if old[k] is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = old[k]
+
+
+def _game(params):
     import astra_cuda as astra
     astra.register_games()
-    old = os.environ.get("ASTRA_MARKET_STAGE_BUDGET")
-    if stage_budget is not None:  # read when the game's market is created
-        os.environ["ASTRA_MARKET_STAGE_BUDGET"] = str(stage_budget)
-    try:
-        return astra.load_game("high_low_trading", params)
-    finally:
-        if stage_budget is not None:
-            if old is None:
-                del os.environ["ASTRA_MARKET_STAGE_BUDGET"]
-            else:
-                os.environ["ASTRA_MARKET_STAGE_BUDGET"] = old
+    return astra.load_game("high_low_trading", params)
 
 
 def _compare(o, s, where):
@@ -58,22 +74,26 @@ def _params(N, P, T, S, cM, V, shape):
     return p
 
 
-@pytest.mark.parametrize("N,P,T,S,cM,V,shape,seed,budget", [
-    (500, 5, 4, 5, 5, 30, None, 1, None),
-    (300, 4, 6, 3, 4, 20, (21, 12, 6, 4), 2, None),         # ring of 12: slot reuse
-    (2000, 5, 3, 5, 5, 127, (128, 1024, 10, 16), 3, None),  # the config-5 shape
-    (300, 8, 3, 5, 5, 30, None, 4, 1),     # 8 and 9 players, staging forced
-    (300, 9, 3, 5, 5, 30, None, 5, 1),
-    (300, 5, 8, 3, 4, 20, (21, 12, 6, 5), 6, 1),
-    (37, 7, 4, 5, 5, 30, None, 7, None),   # 7 players: the observation's tile of 64 envs, ragged
-    (33, 10, 3, 5, 5, 30, None, 8, None),  # 10 (the most): the per-element observation kernel
+@pytest.mark.parametrize("N,P,T,S,cM,V,shape,seed,budget,knobs", [
+    (500, 5, 4, 5, 5, 30, None, 1, None, {}),
+    (300, 4, 6, 3, 4, 20, (21, 12, 6, 4), 2, None, {}),         # ring of 12: slot reuse
+    (2000, 5, 3, 5, 5, 127, (128, 1024, 10, 16), 3, None, {}),  # the config-5 shape
+    (300, 8, 3, 5, 5, 30, None, 4, 1, {}),     # 8 and 9 players, staging forced
+    (300, 9, 3, 5, 5, 30, None, 5, 1, {}),
+    (300, 5, 8, 3, 4, 20, (21, 12, 6, 5), 6, 1, {}),
+    (37, 7, 4, 5, 5, 30, None, 7, None, {}),   # 7 players: the observation's tile of 64 envs, ragged
+    (33, 10, 3, 5, 5, 30, None, 8, None, {}),  # 10 (the most): the per-element observation kernel
+    # the fused move as a large game launches it: 64 envs per wavefront, 4 fill rows
+    (2000, 5, 3, 5, 5, 127, (128, 1024, 10, 16), 9, None, {"per_wave": 64, "fill_rows": 4}),
+    (300, 5, 8, 3, 4, 20, (21, 12, 6, 5), 10, 1, {"per_wave": 64, "fill_rows": 4}),
 ])
-def test_gpu_game_vs_oracle(N, P, T, S, cM, V, shape, seed, budget):
-    print(f"game N={N} P={P} T={T} shape={shape} stage budget {budget}", flush=True)
+def test_gpu_game_vs_oracle(N, P, T, S, cM, V, shape, seed, budget, knobs):
+    print(f"game N={N} P={P} T={T} shape={shape} stage budget {budget} {knobs}", flush=True)
     rng = np.random.default_rng(seed)
     o = OracleHighLow(N, P, T, S, cM, V, market_shape=shape)
-    g = _game(_params(N, P, T, S, cM, V, shape), budget)
-    s = g.new_initial_state()
+    g = _game(_params(N, P, T, S, cM, V, shape))
+    with _engine_knobs(stage_budget=budget, **knobs):
+        s = g.new_initial_state()
     chance, moves = random_game(rng, N, P, T, S, cM, V)
     for c in chance:
         assert s.is_chance_node() and s.current_player() == -1
