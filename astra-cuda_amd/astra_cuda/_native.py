@@ -39,8 +39,8 @@ PROTOTYPES = {
     "astra_market_to_string": (_c_int, [_vp, _c_i32, ctypes.c_char_p, _sz, ctypes.POINTER(_sz),
                                         _vp]),
     "astra_market_set_stats": (_c_int, [_vp, _vp]),
-    "astra_market_get_tid": (_c_int, [_vp, ctypes.POINTER(_c_i32)]),
-    "astra_market_set_tid": (_c_int, [_vp, _c_i32]),
+    "astra_market_get_tid": (_c_int, [_vp, ctypes.POINTER(_c_i32), _vp]),
+    "astra_market_set_tid": (_c_int, [_vp, _c_i32, _vp]),
     "astra_market_shape": (_c_int, [_vp] + [ctypes.POINTER(_c_i32)] * 5),
     "astra_high_low_trade": (_c_int, [_vp, _vp, _vp]),
     "astra_high_low_trade_scratch": (_c_int, [_vp, _vp, _vp]),

@@ -550,7 +550,15 @@ class VecMarket:
 
     @property
     def global_tid(self) -> int:
-        """The host TID counter (market.h:338): base TID of the next call."""
+        """The TID counter (market.h:338): base TID of the next call. It lives in
+        device memory (the matching kernel moves it on), so reading it
+        synchronises the current stream."""
         v = ctypes.c_int32(0)
-        _check(self._lib.astra_market_get_tid(self._h, ctypes.byref(v)))
+        with torch.cuda.device(self._device):
+            _check(self._lib.astra_market_get_tid(self._h, ctypes.byref(v), _raw_stream(self._device_index)))
         return int(v.value)
+
+    @global_tid.setter
+    def global_tid(self, tid: int) -> None:
+        with torch.cuda.device(self._device):
+            _check(self._lib.astra_market_set_tid(self._h, int(tid), _raw_stream(self._device_index)))

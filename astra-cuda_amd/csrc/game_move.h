@@ -202,3 +202,10 @@ int astra_game_move(astra_market *market, const GameMove &g, int32_t *const fill
 
 // The device the market lives on.
 int astra_game_device(const astra_market *market);
+
+// The word of the library's per-device scratch that the market's allocation-free
+// moves use (-1 until its first such move), its assignment, and the release of a
+// word when its market is destroyed (implemented in high_low.hip).
+int astra_game_scratch_word(const astra_market *market);
+void astra_game_set_scratch_word(astra_market *market, int word);
+void astra_game_release_scratch_word(int device, int word);

@@ -297,12 +297,14 @@ const char *check_text(int32_t bits) {  // the first failed check, as the refere
 
 }  // namespace
 
-// The error word of astra_high_low_trade_scratch: the library's own device
+// The error words of astra_high_low_trade_scratch: the library's own device
 // memory, so that its callers need not allocate any. Each GPU holds its own copy
 // at its own address (kept per device in g_scratch after hipGetSymbolAddress);
 // in host code the array's name is not a device address and is never used as
-// one. Word 0 holds the failed checks' bits of the call in flight; the other
-// words are unused. Every call on a GPU shares that GPU's copy.
+// one. Each market that makes such a move gets a word of its own for the failed
+// checks' bits of its moves (and an event of its own for their completion), so
+// moves of different markets never share one; at most kScratchWords live
+// markets per GPU, a destroyed market's word goes back to the pool.
 constexpr int kScratchWords = 64;
 #ifdef ASTRA_HOST_EMULATION
 static int32_t scratch[kScratchWords];  // the host build keeps its "device" memory on the host
@@ -314,15 +316,18 @@ namespace {
 
 constexpr int kMaxScratchDevices = 64;
 struct ScratchDevice {
-  int32_t *ptr = nullptr;   // device address of `scratch` on this device
-  hipEvent_t ev = nullptr;  // the checks' completion event of this device
+  int32_t *ptr = nullptr;               // device address of `scratch` on this device
+  hipEvent_t ev[kScratchWords] = {};    // the checks' completion event of each word
+  uint64_t used = 0;                    // words held by live markets
 };
 ScratchDevice g_scratch[kMaxScratchDevices];
 std::mutex g_scratch_mu;
 
-// Set-up, once per device with that device current: the address of its copy of
-// `scratch` and an event, so the calls themselves allocate nothing.
-int scratch_device(int dev, ScratchDevice **out) {
+// Set-up, once per device with that device current (the device's first
+// allocation-free move): the address of its copy of `scratch` and one event per
+// word, so that the calls themselves allocate nothing. Then the market's word,
+// assigned on its first such move.
+int scratch_word(astra_market *market, int dev, ScratchDevice **out, int *word) {
   if (dev < 0 || dev >= kMaxScratchDevices)
     return fail(ASTRA_ERR_INVALID_ARGUMENT, "astra_high_low_trade_scratch: device id out of range");
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -336,13 +341,26 @@ int scratch_device(int dev, ScratchDevice **out) {
     int32_t *p = nullptr;
     ASTRA_HIP_CHECK(hipGetSymbolAddress(reinterpret_cast<void **>(&p), HIP_SYMBOL(scratch)),
                     "hipGetSymbolAddress(scratch)");
-    hipEvent_t ev = nullptr;
-    ASTRA_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreateWithFlags");
-    d.ev = ev;
+    for (int i = 0; i < kScratchWords; ++i)
+      if (!d.ev[i])
+        ASTRA_HIP_CHECK(hipEventCreateWithFlags(&d.ev[i], hipEventDisableTiming),
+                        "hipEventCreateWithFlags");
     d.ptr = p;
 #endif
   }
+  int w = astra_game_scratch_word(market);
+  if (w < 0) {
+    if (d.used == ~0ull)
+      return fail(ASTRA_ERR_INVALID_ARGUMENT,
+                  "astra_high_low_trade_scratch: all " + std::to_string(kScratchWords) +
+                      " scratch words of device " + std::to_string(dev) +
+                      " are held by live markets");
+    w = __builtin_ctzll(~d.used);
+    d.used |= 1ull << w;
+    astra_game_set_scratch_word(market, w);
+  }
   *out = &d;
+  *word = w;
   return ASTRA_OK;
 }
 
@@ -401,17 +419,16 @@ int trade_impl(astra_market *market, const astra_hl_trade *t, int32_t *errors, h
   hipStream_t s = as_stream(stream);
   DeviceGuard dg(astra_game_device(market));
   // With checks (the reference's behaviour, :264-271): a check launch, the error
-  // word to the host, then the move, which leaves every env as it is when any
-  // check failed. The host waits for the checks (with errors_host, only for
-  // them: the move runs meanwhile) and, on a failed check, restores the TID
-  // counter too, so the call has changed nothing when it returns the error.
+  // word to the host, then the move, which leaves every env as it is, and the
+  // TID counter too, when any check failed; so the call has changed nothing when
+  // it returns the error. The host waits for the checks (with errors_host, only
+  // for them: the move runs meanwhile).
   g.abort_on_error = t->check ? 1 : 0;
-  int32_t tid_before = 0, bits = 0;
+  int32_t bits = 0;
   StreamMark checked;
   checked.ev = ev;
   if (t->check) {
     if ((rc = launch_check(g, M, s))) return rc;
-    if ((rc = astra_market_get_tid(market, &tid_before))) return rc;
     if (t->errors_host) {
       ASTRA_HIP_CHECK(rt_memcpy(t->errors_host, errors, sizeof(int32_t), s), "error flags copy");
       ASTRA_HIP_CHECK(checked.record(s), "error flags event");
@@ -428,7 +445,6 @@ int trade_impl(astra_market *market, const astra_hl_trade *t, int32_t *errors, h
     ASTRA_HIP_CHECK(rt_sync(s), "error flags wait");
   }
   if (bits) {
-    astra_market_set_tid(market, tid_before);
     return fail(ASTRA_ERR_INVALID_ARGUMENT, std::string("high_low_trading.cc ") + check_text(bits));
   }
   return ASTRA_OK;
@@ -455,12 +471,23 @@ int astra_high_low_trade_scratch(astra_market *market, const astra_hl_trade *t, 
                 "astra_high_low_trade_scratch: errors_host (one int32 of pinned host memory) is "
                 "required");
   ScratchDevice *d = nullptr;
-  int rc = scratch_device(astra_game_device(market), &d);
+  int w = 0;
+  int rc = scratch_word(market, astra_game_device(market), &d, &w);
   if (rc) return rc;
-  // word 0 starts at zero: a fill kernel (the last call left its bits there)
-  if ((rc = astra_fill_i32(d->ptr, 1, 0, stream))) return rc;
-  return trade_impl(market, t, d->ptr, d->ev, stream);
+  // the market's word starts at zero: a fill kernel (its last move left its bits there)
+  if ((rc = astra_fill_i32(d->ptr + w, 1, 0, stream))) return rc;
+  return trade_impl(market, t, d->ptr + w, d->ev[w], stream);
 }
+
+}  // extern "C"
+
+void astra_game_release_scratch_word(int device, int word) {
+  if (device < 0 || device >= kMaxScratchDevices || word < 0 || word >= kScratchWords) return;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  g_scratch[device].used &= ~(1ull << word);
+}
+
+extern "C" {
 
 int astra_high_low_rewards(const int32_t *src, int64_t num_envs, int32_t players, int32_t player,
                            float *dst, void *stream) {

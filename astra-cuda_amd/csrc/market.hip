@@ -72,19 +72,30 @@ inline int mask_words_for(int32_t L) {
   return 16;
 }
 
+// Control words at the start of the workspace (int32): the TID counter of a
+// market with no markets (market.h:338; with markets it lives in Book::tids),
+// and the number of helper wavefronts that gave up waiting (a diagnostic count).
+constexpr int kCtlTid = 0;
+constexpr int kCtlHelperExits = 1;
+constexpr size_t kCtlBytes = 256;
+
 // Byte offsets of the book arrays inside the workspace.
 struct Layout {
   int W;
-  size_t masks, next_slot, bbo, tob, hsz, levels, records, portfolios, total;
+  size_t ctl, masks, next_slot, tids, bbo, tob, hsz, levels, records, portfolios, total;
 };
 
 Layout make_layout(int64_t M, int64_t L, int64_t O, int64_t C) {
   Layout l;
   l.W = mask_words_for((int32_t)L);
   size_t off = 0;
+  l.ctl = off;
+  off += kCtlBytes;
   l.masks = off;
   off = align_up(off + (size_t)2 * l.W * M * 8, 256);
   l.next_slot = off;
+  off = align_up(off + (size_t)M * 4, 256);
+  l.tids = off;
   off = align_up(off + (size_t)M * 4, 256);
   l.bbo = off;
   off = align_up(off + (size_t)2 * M * 4, 256);
@@ -109,7 +120,6 @@ struct astra_market {
   int device;
   int32_t threads_per_block;  // validated, not used for launches
   int32_t flags;
-  int32_t tid;                // host TID counter, market.h:338
   int block;                  // launch block size of the per-market kernels
   int32_t stage_budget;       // loop passes before a market is staged in LDS (0: never)
   int32_t lds_limit;          // LDS bytes a workgroup may use on the device
@@ -120,6 +130,8 @@ struct astra_market {
   int32_t helpers;            // market wavefronts per helper wavefront (0: no helpers)
   int32_t hand_lanes;         // zero-size walks go to the helper when at most this many lanes loop
   int32_t hand_queue;         // no hand-off while this many markets wait for the helper
+  int32_t helper_polls;       // idle polls before a helper wavefront gives up
+  int32_t scratch_word;       // word of the per-device scratch its allocation-free moves use (-1: none)
   unsigned long long *stats;  // see astra_market_set_stats
   char *ws;
   size_t ws_bytes;
@@ -129,8 +141,10 @@ struct astra_market {
 namespace {
 
 struct Book {
+  int32_t *ctl;               // the control words (kCtl*)
   uint64_t *masks;            // [2][W][M]: side 0 = bid, 1 = ask
   int32_t *next_slot;         // [M], in [0, O)
+  int32_t *tids;              // [M]: the TID counter (market.h:338), one copy per market
   int32_t *bbo;               // [2][M]: best bid price, best ask price (NULL: empty side)
   uint32_t *tob;              // [M]: head slots of the best levels, bid | ask << 16, each
                               // with kSizeKnown set when its size is in hsz
@@ -144,8 +158,10 @@ struct Book {
 
 Book book_of(const astra_market *h) {
   Book b;
+  b.ctl = reinterpret_cast<int32_t *>(h->ws + h->lay.ctl);
   b.masks = reinterpret_cast<uint64_t *>(h->ws + h->lay.masks);
   b.next_slot = reinterpret_cast<int32_t *>(h->ws + h->lay.next_slot);
+  b.tids = reinterpret_cast<int32_t *>(h->ws + h->lay.tids);
   b.bbo = reinterpret_cast<int32_t *>(h->ws + h->lay.bbo);
   b.tob = reinterpret_cast<uint32_t *>(h->ws + h->lay.tob);
   b.hsz = reinterpret_cast<int32_t *>(h->ws + h->lay.hsz);
@@ -165,7 +181,6 @@ Book book_of(const astra_market *h) {
 // move rows and the acting player in `game`.
 struct QuoteIn {
   const int32_t *bid_px, *bid_sz, *ask_px, *ask_sz, *cust;
-  int32_t base_tid;
   GameMove game;
 };
 
@@ -189,7 +204,7 @@ struct StepOut {
 };
 
 // The quotes and per-step outputs of step k of a multi-step call: the [steps, M]
-// inputs at row k, TID base advanced by 2 per step (market.cu:531).
+// inputs at row k.
 ASTRA_HD void step_views(const QuoteIn &in, const StepOut &so, int64_t M, int32_t steps, int32_t k,
                          QuoteIn &ink, StepOut &sok) {
   const int64_t off = (int64_t)k * M;
@@ -199,7 +214,6 @@ ASTRA_HD void step_views(const QuoteIn &in, const StepOut &so, int64_t M, int32_
   ink.ask_px = in.ask_px + off;
   ink.ask_sz = in.ask_sz + off;
   ink.cust = in.cust + off;
-  ink.base_tid = (int32_t)((uint32_t)in.base_tid + 2u * (uint32_t)k);
   sok.counts = so.counts ? so.counts + off : nullptr;
   for (int j = 0; j < 4; ++j)
     sok.bbo[j] = so.bbo[0] ? so.bbo[0] + ((int64_t)j * steps * M + off) : nullptr;
@@ -546,6 +560,7 @@ struct MarketCtx {
   uint4 *rec;
   int32_t *pf;
   int32_t ns;             // ring position after the inserts
+  int32_t tid;            // the call's TID base (bid: tid, ask: tid + 1)
   bool bid_ok, ask_ok;
   bool keep_b, keep_a;    // a head the call left untouched whose size the cache holds
   GameQuote gq;           // the game's move (GAME only)
@@ -580,7 +595,7 @@ template <int W>
 struct Carry {
   static constexpr bool kState = W <= 4;
   uint64_t bm[W], am[W];
-  int32_t ns, bsz, asz;
+  int32_t ns, tid, bsz, asz;
   uint32_t tob;
   int32_t q[5];
   bool state, quotes;
@@ -726,10 +741,12 @@ ASTRA_HD MarketCtx uniform_ctx(const MarketCtx &a) {
 // the top of a pass into a slot of an LDS queue and leaves the market to the
 // helper, which finishes it from an LDS copy of the book while the market
 // wavefront goes on with its other lanes. Per market wavefront the queue has
-// kHandSlots slots of kSlotWords words, each with a flag word (0 free, 1
-// ready); then one done word per market wavefront.
+// kHandSlots slots of kSlotWords words, each with a flag word (kSlotFree,
+// kSlotReady, or kSlotClosed once the helper has gone); then one done word per
+// market wavefront.
 constexpr int kHandSlots = 4;
 constexpr int kSlotWords = 48;
+constexpr uint32_t kSlotFree = 0u, kSlotReady = 1u, kSlotClosed = 2u;
 
 // Never hands off (every kernel without helpers, and the host build).
 struct NoHand {
@@ -740,7 +757,7 @@ struct NoHand {
 // words: what the helper needs to resume the loop and end the call.
 template <int W>
 ASTRA_HD void pack_slot(uint32_t *p, const LoopState<W> &s, const MarketCtx &c) {
-  static_assert(4 * W + 27 <= kSlotWords, "slot too small for the masks");
+  static_assert(4 * W + 28 <= kSlotWords, "slot too small for the masks");
   int i = 0;
 #pragma unroll
   for (int w = 0; w < W; ++w) {
@@ -778,6 +795,7 @@ ASTRA_HD void pack_slot(uint32_t *p, const LoopState<W> &s, const MarketCtx &c) 
   p[i++] = (uint32_t)c.m;
   p[i++] = (uint32_t)((uint64_t)c.m >> 32);
   p[i++] = (uint32_t)c.ns;
+  p[i++] = (uint32_t)c.tid;
 }
 
 // The inverse of pack_slot; the rest of the context follows from the book.
@@ -820,6 +838,7 @@ ASTRA_HD void unpack_slot(const uint32_t *p, const Book &b, LoopState<W> &s, Mar
   c.m = (int64_t)((uint64_t)p[i] | ((uint64_t)p[i + 1] << 32));
   i += 2;
   c.ns = (int32_t)p[i++];
+  c.tid = (int32_t)p[i++];
   c.L = b.L;
   c.O = b.O;
   c.F = b.F;
@@ -856,7 +875,10 @@ __device__ __forceinline__ bool opaque(bool v) {
 // Called at the top of a pass by the lanes still in their loop (records loaded,
 // nothing of the pass done). Lanes that want to hand off take the free slots in
 // lane order; a lane that gets one writes its buffered rows, packs its state and
-// publishes the slot. Lanes left without a slot go on and ask again next pass.
+// publishes the slot with a compare-and-swap from free to ready, which fails
+// only when the helper has closed the slot meanwhile (it gave up waiting, below):
+// the lane then keeps its market. Lanes left without a slot go on and ask again
+// next pass.
 template <int W, class Sink>
 __device__ bool hand_off(Hand &h, bool want, const LoopState<W> &s, const MarketCtx &c, Sink &sink,
                          const FillOut &out) {
@@ -890,7 +912,10 @@ __device__ bool hand_off(Hand &h, bool want, const LoopState<W> &s, const Market
   pack_slot<W>(h.slots + j * kSlotWords, s, c);
   // the book's writes, the rows and the slot before the flag
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __hip_atomic_store(h.flags + j, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  uint32_t expect = kSlotFree;
+  if (!__hip_atomic_compare_exchange_strong(h.flags + j, &expect, kSlotReady, __ATOMIC_RELAXED,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
+    return false;  // closed: the helper has gone, the lane goes on with its market
   h.handed = true;
   return true;
 }
@@ -961,6 +986,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
       s.am[i] = cy->am[i];
     }
     ns = cy->ns;
+    c.tid = cy->tid;
     tob = cy->tob;
     bsz0 = cy->bsz;
     asz0 = cy->asz;
@@ -971,6 +997,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
       s.am[i] = b.masks[(int64_t)(W + i) * M + m];
     }
     ns = b.next_slot[m];
+    c.tid = b.tids[m];
     tob = b.tob[m];
   }
   GameSnap snap;
@@ -1031,7 +1058,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   if (bid_ok) {
     bslot = (uint32_t)ns;
     ns = (ns + 1 == O) ? 0 : ns + 1;
-    krb = make_uint4((uint32_t)bid_sz, (uint32_t)cust, (uint32_t)in.base_tid,
+    krb = make_uint4((uint32_t)bid_sz, (uint32_t)cust, (uint32_t)c.tid,
                      (uint32_t)bid_px | (kNull16 << 16));
     rec[bslot] = krb;
     const uint32_t old_tail = bword >> 16;
@@ -1049,7 +1076,7 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   if (ask_ok) {
     aslot = (uint32_t)ns;
     ns = (ns + 1 == O) ? 0 : ns + 1;
-    kra = make_uint4((uint32_t)ask_sz, (uint32_t)cust, (uint32_t)((uint32_t)in.base_tid + 1u),
+    kra = make_uint4((uint32_t)ask_sz, (uint32_t)cust, (uint32_t)((uint32_t)c.tid + 1u),
                      (uint32_t)ask_px | (kNull16 << 16));
     rec[aslot] = kra;
     const uint32_t old_tail = aword >> 16;
@@ -1401,6 +1428,7 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
       b.masks[(int64_t)(W + i) * M + m] = s.am[i];
     }
     b.next_slot[m] = c.ns;
+    b.tids[m] = (int32_t)((uint32_t)c.tid + 2u);  // market.cu:531
   }
   sink.flush(out, c.pf, c.C);  // overlaps the loads above
   const bool bv = s.bb >= 0 && s.bh < (uint32_t)O, av = s.ba < L && s.ah < (uint32_t)O;
@@ -1430,6 +1458,7 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
       cy->am[i] = s.am[i];
     }
     cy->ns = c.ns;
+    cy->tid = (int32_t)((uint32_t)c.tid + 2u);
     cy->tob = tob;
     cy->bsz = obs;
     cy->asz = oas;
@@ -1537,6 +1566,23 @@ __device__ __forceinline__ T *in_vgpr(T *p) {
 #else
   return p;
 #endif
+}
+
+// ---- the TID counter in device memory ----
+//
+// The reference keeps one TID counter on the host and passes the base as a
+// kernel argument (market.cu:520,531), which a launch captured in a HIP graph
+// would replay frozen. Here every market keeps the counter in a word of its own
+// (Book::tids): a call reads it with the market's other coalesced words and
+// writes it back advanced in its epilogue. Every call steps every market, so
+// all the words hold the same value, the reference's counter; no lane waits on
+// another and a captured launch replays with advancing TIDs.
+
+// The counter's advance of a call on zero markets (no matching launch).
+__global__ void tid_advance_kernel(int32_t *ctl, int32_t by) {
+  if (threadIdx.x == 0)
+    __hip_atomic_store(ctl + kCtlTid, (int32_t)((uint32_t)ctl[kCtlTid] + (uint32_t)by),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Writes the rows owed by fast-forwarded markets of this wavefront: each such
@@ -1657,7 +1703,7 @@ __device__ void finish_staged(const Book &b, const FillOut &out, int32_t *stage,
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int32_t n = __shfl(rb.n, src);
     const int64_t base = shfl_i64(rb.base, src);
-    done = __shfl(fin, src) != 0;
+    done = uni(__shfl(fin, src) != 0);
     flush_rows(out, rows, srec, n, base, pfm, b.C, lane, 64);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1676,9 +1722,10 @@ __device__ void finish_staged(const Book &b, const FillOut &out, int32_t *stage,
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Polls before a helper wavefront with nothing left to wait for gives up: far
-// beyond any market wavefront's lifetime (each poll sleeps about 0.1 us), it
-// only bounds the kernel if a market wavefront never signalled its end.
+// Idle polls before a helper wavefront gives up waiting (the default of the
+// launch's `helper_polls`): far beyond any market wavefront's lifetime (each
+// poll sleeps about 0.1 us), it only bounds the kernel if a market wavefront
+// never signalled its end.
 constexpr int32_t kHelperMaxPolls = 1 << 22;
 
 // The helper wavefront of a workgroup with H market wavefronts: takes ready
@@ -1686,45 +1733,56 @@ constexpr int32_t kHelperMaxPolls = 1 << 22;
 // read, finishes the market (finish_staged, lane 0 walking) and writes its
 // repeating rows; returns when every market wavefront has signalled its end and
 // no slot is ready.
+//
+// After `max_polls` idle polls in a row it gives up instead: it closes every
+// free slot (a compare-and-swap from free to closed, so a market lane's
+// publication either comes first and is finished here, or fails and the lane
+// keeps its market), finishes the markets already published, counts the
+// give-up in the workspace's control words and returns. Every market is then
+// finished, by the helper or in global memory by its own lane.
 template <int W, int H>
 __device__ void helper_wave(const Book &b, const FillOut &out, int32_t *stage, uint32_t *slots,
-                            uint32_t *flags, const uint32_t *done, int lane) {
+                            uint32_t *flags, const uint32_t *done, int lane, int32_t max_polls) {
   uint32_t *busy = flags + H * kHandSlots;  // 1 while a market is being finished
   FillSink<4> sink;  // never buffers a row: the epilogue's flush finds it empty
 #if defined(__HIP_DEVICE_COMPILE__)
   sink.lds = stage;
   sink.lane = lane;
 #endif
+  // finishes the market in slot j; the slot becomes `after` once it is read
+  auto take = [&](int j, uint32_t after) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    LoopState<W> st;
+    MarketCtx c;
+    unpack_slot<W>(slots + j * kSlotWords, b, st, c);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0) {
+      __hip_atomic_store(busy, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_store(flags + j, after, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    sink.n = 0;
+    sink.base = c.m * (int64_t)b.F + st.fc;
+    Bulk bulk;
+    bulk.count = 0;
+    finish_staged<W, false, false, false>(b, out, stage, lane, 0, c.m, c, st, sink, bulk,
+                                          GameMove{}, StepOut{}, (Carry<W> *)nullptr, true);
+    if (lane != 0) bulk.count = 0;
+    write_bulk_wave(out, bulk);
+    if (lane == 0) __hip_atomic_store(busy, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
   int32_t polls = 0;
   for (;;) {
     uint32_t ready = 0;
 #pragma unroll
     for (int j = 0; j < H * kHandSlots; ++j)
-      ready |= (__hip_atomic_load(flags + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 1u
+      ready |= (__hip_atomic_load(flags + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+                        kSlotReady
                     ? 1u
                     : 0u)
                << j;
     ready = uni(ready);
     if (ready) {
-      const int j = __ffs(ready) - 1;
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      LoopState<W> st;
-      MarketCtx c;
-      unpack_slot<W>(slots + j * kSlotWords, b, st, c);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      if (lane == 0) {
-        __hip_atomic_store(busy, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        __hip_atomic_store(flags + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
-      sink.n = 0;
-      sink.base = c.m * (int64_t)b.F + st.fc;
-      Bulk bulk;
-      bulk.count = 0;
-      finish_staged<W, false, false, false>(b, out, stage, lane, 0, c.m, c, st, sink, bulk,
-                                            GameMove{}, StepOut{}, (Carry<W> *)nullptr, true);
-      if (lane != 0) bulk.count = 0;
-      write_bulk_wave(out, bulk);
-      if (lane == 0) __hip_atomic_store(busy, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      take(__ffs(ready) - 1, kSlotFree);
       polls = 0;
       continue;
     }
@@ -1742,9 +1800,30 @@ __device__ void helper_wave(const Book &b, const FillOut &out, int32_t *stage, u
       if (uni(left) == 0u) return;
       continue;
     }
-    if (++polls > kHelperMaxPolls) return;
+    if (uni(++polls) > max_polls) break;
     __builtin_amdgcn_s_sleep(2);
   }
+  // Give up: lane 0 closes every free slot (one compare-and-swap each); a slot
+  // that was ready instead is finished here and closed once read. After this
+  // one pass no slot can become ready, so the wavefront finishes the ones found
+  // ready in a loop over a wave-uniform mask (every lane takes part in
+  // finish_staged's cooperative copy; a loop whose condition the compiler
+  // takes for divergent has run the second finish on lane 0 alone).
+  uint32_t ready = 0;
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < H * kHandSlots; ++j) {
+      uint32_t expect = kSlotFree;
+      if (!__hip_atomic_compare_exchange_strong(flags + j, &expect, kSlotClosed, __ATOMIC_RELAXED,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) &&
+          expect == kSlotReady)
+        ready |= 1u << j;
+    }
+  }
+  for (uint32_t pending = uni((uint32_t)__shfl((int32_t)ready, 0)); pending; pending &= pending - 1u)
+    take(__ffs(pending) - 1, kSlotClosed);
+  if (lane == 0)
+    __hip_atomic_fetch_add(b.ctl + kCtlHelperExits, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Fused add + match + BBO, one lane per market, in two passes.
@@ -1779,7 +1858,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
                                                           StepOut so, int32_t steps,
                                                           int32_t budget, int32_t wave_words,
                                                           int32_t per_wave, int32_t hand_lanes,
-                                                          int32_t hand_queue) {
+                                                          int32_t hand_queue, int32_t helper_polls) {
   constexpr bool kApart = FR == 2;  // the staged book beside the row buffer
   static_assert(HELP == 0 || (!STATS && !GAME && !MULTI && FR == 4 && W <= 4),
                 "helpers serve plain single-step calls of large grids");
@@ -1818,7 +1897,7 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
     if (threadIdx.x < HELP * (kHandSlots + 1) + 1) flags[threadIdx.x] = 0u;
     __syncthreads();
     if (wv == HELP) {
-      helper_wave<W, HELP>(b, out, stage, slots, flags, done, lane);
+      helper_wave<W, HELP>(b, out, stage, slots, flags, done, lane, helper_polls);
       return;
     }
     hand.slots = slots + wv * kHandSlots * kSlotWords;
@@ -1999,6 +2078,7 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   const int32_t rows_cap = (MULTI || !fits_apart) ? 4 : fill_rows_per_flush(h, waves_per_cu);
 #ifdef ASTRA_HOST_EMULATION
   (void)s;
+  const QuoteIn &inb = in;
   std::vector<uint4> srec(staged ? (size_t)h->O : 0);
   std::vector<uint16_t> slv(staged ? (size_t)h->L * 4 : 0);
   std::vector<uint4> rows((size_t)kStageRows);
@@ -2013,7 +2093,7 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
     LoopState<W> st;
     Carry<W> *cy = MULTI ? &carry[(size_t)m] : nullptr;
     quote_prologue<W, GAME, MULTI>(b, ink, m, c, st, cy);
-    if (MULTI) load_next_quotes(in, b.M, k + 1, steps, m, *cy);
+    if (MULTI) load_next_quotes(inb, b.M, k + 1, steps, m, *cy);
     if (GAME && c.abort) return;
     sink.base = m * (int64_t)b.F;
     const GlobalBook gb{c.lv, c.rec};
@@ -2048,9 +2128,9 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
     if (bulk.count > 0) write_bulk_host(fo, bulk);
   };
   for (int32_t k = 0; k < (MULTI ? steps : 1); ++k) {
-    QuoteIn ink = in;
+    QuoteIn ink = inb;
     StepOut sok = so;
-    if (MULTI) step_views(in, so, b.M, steps, k, ink, sok);
+    if (MULTI) step_views(inb, so, b.M, steps, k, ink, sok);
     const bool last = k + 1 == (MULTI ? steps : 1);
     for (int64_t m = 0; m < b.M; ++m) {
       if (rows_cap == 2) market(FillSink<2>{}, ink, sok, k, last, m);
@@ -2077,11 +2157,11 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
     if (fo.rows)                                                                                \
       hipLaunchKernelGGL((quote_match_kernel<W, false, false, false, true, 4, H_>), grid_h,     \
                          block_h, lds_h, s, b, in, fo, so, steps, budget, ww, per_wave,         \
-                         h->hand_lanes, h->hand_queue);                         \
+                         h->hand_lanes, h->hand_queue, h->helper_polls);                         \
     else                                                                                        \
       hipLaunchKernelGGL((quote_match_kernel<W, false, false, false, false, 4, H_>), grid_h,    \
                          block_h, lds_h, s, b, in, fo, so, steps, budget, ww, per_wave,         \
-                         h->hand_lanes, h->hand_queue);                         \
+                         h->hand_lanes, h->hand_queue, h->helper_polls);                         \
   } while (0)
         if (helpers == 2)
           ASTRA_LAUNCH_HELP(2);
@@ -2102,27 +2182,27 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
   if (b.stats && fo.rows)
     hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI, true, 4>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave, 0, 0);
+                       per_wave, 0, 0, 0);
   else if (b.stats)
     hipLaunchKernelGGL((quote_match_kernel<W, true, GAME, MULTI, false, 4>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave, 0, 0);
+                       per_wave, 0, 0, 0);
   else if (fo.rows && rows_cap == 2 && !MULTI)
     hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, true, MULTI ? 4 : 2>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave, 0, 0);
+                       per_wave, 0, 0, 0);
   else if (fo.rows)
     hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, true, 4>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave, 0, 0);
+                       per_wave, 0, 0, 0);
   else if (rows_cap == 2 && !MULTI)
     hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, false, MULTI ? 4 : 2>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave, 0, 0);
+                       per_wave, 0, 0, 0);
   else
     hipLaunchKernelGGL((quote_match_kernel<W, false, GAME, MULTI, false, 4>), dim3(grid),
                        dim3(h->block), lds, s, b, in, fo, so, steps, budget, wave_words,
-                       per_wave, 0, 0);
+                       per_wave, 0, 0, 0);
 #endif
   ASTRA_HIP_CHECK(rt_last_error(), "AddTwoSidedQuotes");
   return ASTRA_OK;
@@ -2213,14 +2293,28 @@ int launch_last_price(int32_t *last, const int32_t *counts, const int32_t *price
   return ASTRA_OK;
 }
 
-// Empty book: masks 0, slot counters 0, BBO cache empty, level words NULL,
-// portfolios 0 (the
+// The TID counter's advance of a call on zero markets, which launches no
+// matching kernel (the reference moves its counter on whatever M is).
+int advance_tid_empty(astra_market *h, int32_t by, hipStream_t s) {
+  int32_t *ctl = reinterpret_cast<int32_t *>(h->ws + h->lay.ctl);
+#ifdef ASTRA_HOST_EMULATION
+  (void)s;
+  ctl[kCtlTid] = (int32_t)((uint32_t)ctl[kCtlTid] + (uint32_t)by);
+#else
+  hipLaunchKernelGGL(tid_advance_kernel, dim3(1), dim3(64), 0, s, ctl, by);
+#endif
+  ASTRA_HIP_CHECK(rt_last_error(), "AddTwoSidedQuotes");
+  return ASTRA_OK;
+}
+
+// Empty book: TID counter 0, masks 0, slot counters 0, BBO cache empty, level
+// words NULL, portfolios 0 (the
 // order records are left alone: no list reaches a slot before it is written).
 int init_book(astra_market *h, hipStream_t s) {
   const Layout &l = h->lay;
   int rc;
-  if ((rc = launch_fill(h->ws + l.masks, (int64_t)(l.bbo - l.masks) / 4, 0u, s, "init")))
-    return rc;
+  // control words, masks, slot counters and TID counters 0 (market.cu:715)
+  if ((rc = launch_fill(h->ws + l.ctl, (int64_t)(l.bbo - l.ctl) / 4, 0u, s, "init"))) return rc;
   // BBO cache of an empty book: both prices NULL
   int32_t *bbo = reinterpret_cast<int32_t *>(h->ws + l.bbo);
   if ((rc = launch_fill(bbo, 2 * (int64_t)h->M, 0xFFFFFFFFu, s, "init"))) return rc;
@@ -2299,6 +2393,15 @@ int32_t default_hand_queue() {
   return (x >= 1 && x <= 13) ? x : 2;
 }
 
+// ASTRA_MARKET_HELPER_POLLS: idle polls before a helper wavefront gives up
+// waiting (at least 1; a small value makes the helpers leave early, which every
+// result tolerates: a test knob).
+int32_t default_helper_polls() {
+  const char *e = std::getenv("ASTRA_MARKET_HELPER_POLLS");
+  const int x = e ? std::atoi(e) : 0;
+  return x >= 1 ? x : kHelperMaxPolls;
+}
+
 int default_block() {
   const char *e = std::getenv("ASTRA_MARKET_BLOCK");
   if (e) {
@@ -2373,7 +2476,6 @@ int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, i
   h->device = device_id;
   h->threads_per_block = threads_per_block;
   h->flags = flags;
-  h->tid = 0;
   h->block = default_block();
   h->stage_budget = default_stage_budget();
   h->lds_limit = lds_limit;
@@ -2384,6 +2486,8 @@ int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, i
   h->helpers = default_helpers();
   h->hand_lanes = default_hand_lanes();
   h->hand_queue = default_hand_queue();
+  h->helper_polls = default_helper_polls();
+  h->scratch_word = -1;
   h->stats = nullptr;
   h->ws = static_cast<char *>(workspace);
   h->ws_bytes = workspace_bytes;
@@ -2403,6 +2507,7 @@ int astra_market_create(int32_t M, int32_t L, int32_t O, int32_t F, int32_t C, i
 int astra_market_destroy(astra_market *h) {
   if (!h) return ASTRA_OK;
   rt_device_sync(h->device);  // market.cu:416-417
+  if (h->scratch_word >= 0) astra_game_release_scratch_word(h->device, h->scratch_word);
   delete h;
   return ASTRA_OK;
 }
@@ -2420,6 +2525,7 @@ int astra_market_clone(const astra_market *src, void *dst_ws, size_t dst_bytes, 
     ASTRA_HIP_CHECK(rt_memcpy(dst_ws, src->ws, src->lay.total, as_stream(stream)), "clone");
   astra_market *h = new astra_market(*src);
   h->stats = nullptr;
+  h->scratch_word = -1;  // the copy gets a word of its own on its first such move
   h->ws = static_cast<char *>(dst_ws);
   h->ws_bytes = dst_bytes;
   *out = h;
@@ -2442,17 +2548,15 @@ int astra_market_add_two_sided_quotes(astra_market *h, const int32_t *bid_px,
                      !fill_is_sell_quote || !fill_quote_sizes || !fill_tid || !fill_quote_tid))
       return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL fill pointer");
     DeviceGuard g(h->device);
-    const QuoteIn in{bid_px, bid_sz, ask_px, ask_sz, customer_ids, h->tid};
+    const QuoteIn in{bid_px, bid_sz, ask_px, ask_sz, customer_ids};
     const FillOut fo{fill_prices,        fill_sizes,       fill_customer_ids, fill_quoter_ids,
                      fill_is_sell_quote, fill_quote_sizes, fill_tid,          fill_quote_tid,
                      fill_counts,        nullptr};
-    const int rc = [&]() -> int {
-      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_plain, h, in, fo, as_stream(stream));
-    }();
-    if (rc) return rc;
+    // (returns; the kernel moves the TID counter on by 2, market.cu:531)
+    ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_plain, h, in, fo, as_stream(stream));
   }
-  h->tid = (int32_t)((uint32_t)h->tid + 2u);  // market.cu:531
-  return ASTRA_OK;
+  DeviceGuard g(h->device);
+  return advance_tid_empty(h, 2, as_stream(stream));
 }
 
 int astra_market_add_two_sided_quotes_rows(astra_market *h, const int32_t *bid_px,
@@ -2468,17 +2572,15 @@ int astra_market_add_two_sided_quotes_rows(astra_market *h, const int32_t *bid_p
     if ((reinterpret_cast<uintptr_t>(fill_rows) & 15) != 0)
       return fail(ASTRA_ERR_INVALID_ARGUMENT, "fill_rows must be 16-byte aligned");
     DeviceGuard g(h->device);
-    const QuoteIn in{bid_px, bid_sz, ask_px, ask_sz, customer_ids, h->tid};
+    const QuoteIn in{bid_px, bid_sz, ask_px, ask_sz, customer_ids};
     FillOut fo{};
     fo.counts = fill_counts;
     fo.rows = fill_rows;
-    const int rc = [&]() -> int {
-      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_plain, h, in, fo, as_stream(stream));
-    }();
-    if (rc) return rc;
+    // (returns; the kernel moves the TID counter on by 2, market.cu:531)
+    ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_plain, h, in, fo, as_stream(stream));
   }
-  h->tid = (int32_t)((uint32_t)h->tid + 2u);  // market.cu:531
-  return ASTRA_OK;
+  DeviceGuard g(h->device);
+  return advance_tid_empty(h, 2, as_stream(stream));
 }
 
 int astra_market_add_two_sided_quotes_steps(
@@ -2503,7 +2605,7 @@ int astra_market_add_two_sided_quotes_steps(
       return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL fill pointer");
     }
     DeviceGuard g(h->device);
-    const QuoteIn in{bid_px, bid_sz, ask_px, ask_sz, customer_ids, h->tid};
+    const QuoteIn in{bid_px, bid_sz, ask_px, ask_sz, customer_ids};
     FillOut fo{};
     fo.counts = fill_counts;
     if (fill_rows) {
@@ -2516,26 +2618,25 @@ int astra_market_add_two_sided_quotes_steps(
     StepOut so{};
     so.counts = step_fill_counts;
     so.bbo[0] = step_bbos;  // step_views derives the other three fields' rows
-    const int rc = [&]() -> int {
-      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_steps, h, in, fo, so, steps,
-                       as_stream(stream));
-    }();
-    if (rc) return rc;
+    // (returns; the kernel moves the TID counter on by 2 per step, market.cu:531)
+    ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_steps, h, in, fo, so, steps, as_stream(stream));
   }
-  h->tid = (int32_t)((uint32_t)h->tid + 2u * (uint32_t)steps);  // market.cu:531, per step
-  return ASTRA_OK;
+  DeviceGuard g(h->device);
+  return advance_tid_empty(h, (int32_t)(2u * (uint32_t)steps), as_stream(stream));
 }
 
 }  // extern "C"
 
 int astra_game_device(const astra_market *h) { return h ? h->device : 0; }
+int astra_game_scratch_word(const astra_market *h) { return h->scratch_word; }
+void astra_game_set_scratch_word(astra_market *h, int word) { h->scratch_word = word; }
 
 int astra_game_move(astra_market *h, const GameMove &g, int32_t *const fill_fields[8],
                     int32_t *fill_rows, int32_t *fill_counts, hipStream_t stream) {
   if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
   if (h->M > 0) {
     DeviceGuard dg(h->device);
-    QuoteIn in{nullptr, nullptr, nullptr, nullptr, nullptr, h->tid, g};
+    QuoteIn in{nullptr, nullptr, nullptr, nullptr, nullptr, g};
     if ((reinterpret_cast<uintptr_t>(fill_rows) & 15) != 0)
       return fail(ASTRA_ERR_INVALID_ARGUMENT, "fill_rows must be 16-byte aligned");
     FillOut fo{};
@@ -2552,13 +2653,12 @@ int astra_game_move(astra_market *h, const GameMove &g, int32_t *const fill_fiel
       fo.tid = fill_fields[6];
       fo.quote_tid = fill_fields[7];
     }
-    const int rc = [&]() -> int {
-      ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_game, h, in, fo, stream);
-    }();
-    if (rc) return rc;
+    // (returns; the kernel moves the TID counter on by 2, market.cu:531,
+    // unless the move's checks failed)
+    ASTRA_DISPATCH_W(h->lay.W, launch_quote_match_game, h, in, fo, stream);
   }
-  h->tid = (int32_t)((uint32_t)h->tid + 2u);  // market.cu:531
-  return ASTRA_OK;
+  DeviceGuard dg(h->device);
+  return advance_tid_empty(h, 2, stream);
 }
 
 extern "C" {
@@ -2603,10 +2703,7 @@ int astra_fill_i32(int32_t *dst, int64_t count, int32_t value, void *stream) {
 int astra_market_reset(astra_market *h, void *stream) {
   if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
   DeviceGuard g(h->device);
-  const int rc = init_book(h, as_stream(stream));  // market.cu:699-712
-  if (rc) return rc;
-  h->tid = 0;  // market.cu:715
-  return ASTRA_OK;
+  return init_book(h, as_stream(stream));  // market.cu:699-715, the TID counter included
 }
 
 int astra_market_clear_quotes(astra_market *h, const uint8_t *reset, void *stream) {
@@ -2697,16 +2794,24 @@ int astra_market_set_stats(astra_market *h, int64_t *counters) {
   return ASTRA_OK;
 }
 
-int astra_market_get_tid(const astra_market *h, int32_t *tid) {
+int astra_market_get_tid(const astra_market *h, int32_t *tid, void *stream) {
   if (!h || !tid) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL argument");
-  *tid = h->tid;
+  DeviceGuard g(h->device);
+  hipStream_t st = as_stream(stream);
+  // every market's copy holds the counter; a market-less book keeps it in ctl
+  const char *src = h->M > 0 ? h->ws + h->lay.tids : h->ws + h->lay.ctl + kCtlTid * 4;
+  ASTRA_HIP_CHECK(rt_memcpy(tid, src, sizeof(int32_t), st), "get_tid");
+  ASTRA_HIP_CHECK(rt_sync(st), "get_tid");
   return ASTRA_OK;
 }
 
-int astra_market_set_tid(astra_market *h, int32_t tid) {
+int astra_market_set_tid(astra_market *h, int32_t tid, void *stream) {
   if (!h) return fail(ASTRA_ERR_INVALID_ARGUMENT, "NULL handle");
-  h->tid = tid;
-  return ASTRA_OK;
+  DeviceGuard g(h->device);
+  const int rc = launch_fill(h->ws + h->lay.ctl + kCtlTid * 4, 1, (uint32_t)tid, as_stream(stream),
+                             "set_tid");
+  if (rc) return rc;
+  return launch_fill(h->ws + h->lay.tids, h->M, (uint32_t)tid, as_stream(stream), "set_tid");
 }
 
 }  // extern "C"

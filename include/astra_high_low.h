@@ -80,14 +80,17 @@ int astra_high_low_trade(astra_market *market, const astra_hl_trade *t, void *st
 
 /* No counterpart in the reference: astra_high_low_trade for callers that cannot
  * allocate device memory (serving loops, harnesses that forbid hipMalloc). The
- * checks' error word is the library's own per-device scratch (one static device
- * array of 64 int32 per GPU, holding the word whatever N is) instead of
- * t->errors, which is ignored and may be NULL. Requires check = 1 (the word is
+ * checks' error word is a word of the library's own per-device scratch (one
+ * static device array of 64 int32 per GPU) instead of t->errors, which is
+ * ignored and may be NULL: each market gets a word of its own on its first such
+ * move, kept until the market is destroyed, so at most 64 live markets per GPU
+ * use this entry point (the 65th gets an error). Requires check = 1 (the word is
  * cleared by every call, so unchecked moves could not report later) and
  * errors_host (one int32 of pinned host memory). Results and errors are those of
- * astra_high_low_trade. Allocates nothing: the device address of the scratch and
- * an event are set up once per device on its first call there. Calls that
- * overlap on one GPU (other host threads or streams) share its scratch and race. */
+ * astra_high_low_trade. Allocates nothing: the first call on a device sets up
+ * the scratch's device address and one event per word. Moves of different
+ * markets never share a word or an event; moves of one market must be ordered
+ * (one stream, or synchronised), as every call on a market must be. */
 int astra_high_low_trade_scratch(astra_market *market, const astra_hl_trade *t, void *stream);
 
 /* FillObservationTensor(player, values) (high_low_trading.cc:510-602). */

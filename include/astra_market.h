@@ -62,8 +62,8 @@ int astra_market_workspace_size(int32_t num_markets, int32_t max_price_levels,
 
 /* VecMarket::VecMarket (market.cu:326-383; market.h:138-140). Checks the caps
  * (market.cu:338-350) and the device id, then initialises the workspace on
- * `stream` to the empty book: all levels NULL, slot counters 0, portfolios 0;
- * the host TID counter starts at 0. threads_per_block is validated
+ * `stream` to the empty book: all levels NULL, slot counters 0, portfolios 0,
+ * the TID counter (a word of the workspace) 0. threads_per_block is validated
  * (0 < tpb <= 1024) but has no effect on results, as in the reference. */
 int astra_market_create(int32_t num_markets, int32_t max_price_levels,
                         int32_t max_active_orders_per_market, int32_t max_active_fills_per_market,
@@ -76,7 +76,7 @@ int astra_market_create(int32_t num_markets, int32_t max_price_levels,
 int astra_market_destroy(astra_market *market);
 
 /* VecMarket copy constructor (market.cu:385-411): copies the whole book
- * (device-to-device on `stream`) into dst_workspace and the host TID counter. */
+ * (device-to-device on `stream`), TID counter included, into dst_workspace. */
 int astra_market_clone(const astra_market *src, void *dst_workspace, size_t dst_workspace_bytes,
                        void *stream, astra_market **out);
 
@@ -84,7 +84,10 @@ int astra_market_clone(const astra_market *src, void *dst_workspace, size_t dst_
  * Inputs: five int32 [M] device arrays. Outputs: the FillBatch (market.h:64-92),
  * eight [M,F] arrays (fill_is_sell_quote as one byte 0/1) and int32 [M]
  * fill_counts. Adds the bid then the ask of each market (TIDs base, base+1),
- * matches, and advances the host TID counter by 2. */
+ * matches, and advances the TID counter by 2. The base is read from the
+ * workspace by the kernel, not passed by the host: a launch captured in a HIP
+ * graph replays with advancing TIDs (the reference passes it as an argument,
+ * market.cu:520,531; see astra_market_get_tid). */
 int astra_market_add_two_sided_quotes(astra_market *market, const int32_t *bid_px,
                                       const int32_t *bid_sz, const int32_t *ask_px,
                                       const int32_t *ask_sz, const int32_t *customer_ids,
@@ -188,9 +191,16 @@ int astra_market_to_string(const astra_market *market, int32_t market_id, char *
  * off (the default); the timed path never has it on. */
 int astra_market_set_stats(astra_market *market, int64_t *counters);
 
-/* Host TID counter (market.h:338): read, and set (for restoring a snapshot). */
-int astra_market_get_tid(const astra_market *market, int32_t *tid);
-int astra_market_set_tid(astra_market *market, int32_t tid);
+/* The TID counter (market.h:338, the base TID of the next call). The reference
+ * keeps it on the host and passes it to its kernels as an argument
+ * (market.cu:520,531); here every market keeps a copy in the workspace, which
+ * the matching kernel reads and advances with the market's other words, so that
+ * calls captured in a HIP graph replay with advancing TIDs (every call steps
+ * every market, so the copies agree). get: copies it to the host on `stream` and
+ * synchronises the stream. set: writes every copy on `stream` (fill kernels, so
+ * the call can be captured too). */
+int astra_market_get_tid(const astra_market *market, int32_t *tid, void *stream);
+int astra_market_set_tid(astra_market *market, int32_t tid, void *stream);
 
 #ifdef __cplusplus
 }

@@ -224,7 +224,7 @@ class EmuMarket:
     @property
     def global_tid(self):
         v = ctypes.c_int32()
-        _check(lib().astra_market_get_tid(self.h, ctypes.byref(v)))
+        _check(lib().astra_market_get_tid(self.h, ctypes.byref(v), None))
         return v.value
 
 

@@ -112,7 +112,7 @@ def compare_portfolios(gpu_mk, ora_mk, where: str):
 
 
 def make_market(M, L, O, F, C, extended=None, stage_budget=None, per_wave=None, fill_rows=None,
-                helpers=None, hand_lanes=None, hand_queue=None):
+                helpers=None, hand_lanes=None, hand_queue=None, helper_polls=None):
     """VecMarket through the drop-in API. stage_budget (read by the engine when the
     market is created) sets the loop passes before a market's book is staged in
     LDS; 1 forces the staged path for every market that crosses twice. per_wave
@@ -121,14 +121,16 @@ def make_market(M, L, O, F, C, extended=None, stage_budget=None, per_wave=None, 
     wavefronts per helper wavefront (0: none; 2 or 3) where the launch uses
     helpers (4 fill rows, staged books), hand_lanes how few lanes must still loop
     for a zero-size walk to go to the helper, hand_queue how many markets one helper
-    may hold at once."""
+    may hold at once, helper_polls the idle polls after which a helper gives up
+    waiting (closing its queue)."""
     import os
     from astra_cuda import order_matching as aom
     if extended is None:
         extended = L > 128 or O > 1024 or F > 1024 or C > 1024
     env = {"ASTRA_MARKET_STAGE_BUDGET": stage_budget, "ASTRA_MARKET_PER_WAVE": per_wave,
            "ASTRA_MARKET_FILL_ROWS": fill_rows, "ASTRA_MARKET_HELPERS": helpers,
-           "ASTRA_MARKET_HAND_LANES": hand_lanes, "ASTRA_MARKET_HAND_QUEUE": hand_queue}
+           "ASTRA_MARKET_HAND_LANES": hand_lanes, "ASTRA_MARKET_HAND_QUEUE": hand_queue,
+           "ASTRA_MARKET_HELPER_POLLS": helper_polls}
     old = {k: os.environ.get(k) for k in env}
     for k, v in env.items():
         if v is not None:
@@ -147,7 +149,8 @@ def make_market(M, L, O, F, C, extended=None, stage_budget=None, per_wave=None, 
 
 def run_parity(M, L, O, F, C, steps, gen, *, bbo_every=1, full_every=0, last_every=1,
                extended=None, nthreads=8, label="", stage_budget=None, layout="columns",
-               per_wave=None, fill_rows=None, helpers=None, hand_lanes=None, hand_queue=None):
+               per_wave=None, fill_rows=None, helpers=None, hand_lanes=None, hand_queue=None,
+               helper_polls=None):
     """Drive GPU engine and oracle with the same inputs; compare after every step.
 
     ``gen(t)`` returns (bid_px, bid_sz, ask_px, ask_sz, cust) int32 arrays of shape [M].
@@ -155,7 +158,7 @@ def run_parity(M, L, O, F, C, steps, gen, *, bbo_every=1, full_every=0, last_eve
     """
     from oracle.oracle import OracleMarket
     g = make_market(M, L, O, F, C, extended, stage_budget, per_wave, fill_rows, helpers, hand_lanes,
-                    hand_queue)
+                    hand_queue, helper_polls)
     gf, gb = g.new_fill_batch(layout), g.new_bbo_batch()
     o = OracleMarket(M, L, O, F, C)
     of, ob = o.new_fill_batch(), o.new_bbo_batch()
@@ -179,3 +182,10 @@ def run_parity(M, L, O, F, C, steps, gen, *, bbo_every=1, full_every=0, last_eve
             compare_portfolios(g, o, where)
     assert g.global_tid == o.global_tid
     return {"fill_rows": rows, "overflows": overflows, "gpu": g, "oracle": o}
+
+
+def helper_exits(mk) -> int:
+    """Helper wavefronts that gave up waiting so far (the second control word at the
+    start of the engine's workspace)."""
+    torch.cuda.synchronize()
+    return int(mk._ws[4:8].view(torch.int32).item())

@@ -95,6 +95,34 @@ def test_gpu_config3_subset_helpers(helpers, hand_lanes, stage_budget, layout, h
     assert r["fill_rows"] > 4000
 
 
+@pytest.mark.parametrize("helpers,helper_polls", [(2, 1), (3, 1), (2, 8), (3, 64)])
+def test_gpu_config3_subset_helpers_give_up(helpers, helper_polls):
+    """The helper wavefronts' bounded wait, cut short from the host: after
+    helper_polls idle polls a helper closes its workgroup's queue, finishes the
+    markets already handed to it and leaves; lanes that would hand off later keep
+    their markets and finish them in global memory. With 1 poll (about 0.1 us)
+    every helper leaves before its wavefronts can hand anything off; with 8 and
+    64 helpers leave in the middle of a call, some with markets in their queue.
+    Every result must still equal the oracle's, and the give-ups are counted in
+    the workspace."""
+    from parity_util import helper_exits
+    cfg, gen = _stream_gen(3, np.arange(4000))
+    _log(f"config 3 subset, helpers {helpers} giving up after {helper_polls} idle polls")
+    r = run_parity(4000, cfg.L, cfg.O, cfg.F, cfg.C, 1000, gen, bbo_every=1, full_every=250,
+                   label=f"cfg3 helpers give up {helper_polls}", layout="columns", fill_rows=4,
+                   helpers=helpers, per_wave=64, helper_polls=helper_polls)
+    assert r["fill_rows"] > 4000
+    exits = helper_exits(r["gpu"])
+    _log(f"helper give-ups over 1000 calls: {exits}")
+    if helper_polls == 1:
+        # nearly every helper of every call (4000 markets: 63 market wavefronts in
+        # 21 or 32 workgroups; a market wavefront needs two memory round trips
+        # before it can end)
+        assert exits >= 10000
+    elif helper_polls == 8:
+        assert exits > 0
+
+
 @pytest.mark.parametrize("fill_rows,per_wave,stage_budget", [
     (None, None, None), (4, 64, None), (4, 64, 1)])
 def test_gpu_config4_subset_deep_book(fill_rows, per_wave, stage_budget):

@@ -6,7 +6,12 @@ workspace than in the other: a multi-step launch caches the size of every head i
 hands out as a BBO, single calls only those whose order record they hold in
 registers (get_bbos reads the others from the book, so both give the same
 BBOs). ``normalized`` clears the cache's flags (bit 15 of each half of the tob
-word) and its size array, leaving everything else as it is.
+word that holds a slot; an empty head, 0xFFFF, keeps its value) and its size
+array, leaving everything else as it is.
+
+The workspace starts with 256 bytes of control words (int32): the TID counter
+of a book with no markets (otherwise every market keeps a copy in ``tids``) and
+the count of helper wavefronts that gave up waiting.
 """
 from __future__ import annotations
 
@@ -26,7 +31,8 @@ def layout(M: int, L: int, O: int, C: int) -> dict:
     """(byte offset, bytes) of each array of the workspace."""
     W = mask_words(L)
     off, out = 0, {}
-    for name, nbytes in (("masks", 2 * W * M * 8), ("next_slot", M * 4), ("bbo", 2 * M * 4),
+    for name, nbytes in (("ctl", 256), ("masks", 2 * W * M * 8), ("next_slot", M * 4), ("tids", M * 4),
+                         ("bbo", 2 * M * 4),
                          ("tob", M * 4), ("hsz", 2 * M * 4), ("levels", M * L * 8),
                          ("records", M * O * 16), ("portfolios", M * C * 8)):
         out[name] = (off, nbytes)
@@ -44,11 +50,14 @@ def normalized(ws, M: int, L: int, O: int, C: int):
     lay = layout(M, L, O, C)
     o, n = lay["tob"]
     if n:
+        # bit 15 of a half flags a cached size; 0xFFFF (empty) carries no flag
         if is_np:
-            w[o:o + n].view(np.int32)[:] &= 0x7FFF7FFF
+            h = w[o:o + n].view(np.uint16)
+            h[h != 0xFFFF] &= 0x7FFF
         else:
             import torch
-            w[o:o + n].view(torch.int32).bitwise_and_(0x7FFF7FFF)
+            h = w[o:o + n].view(torch.int16)
+            h.copy_(torch.where(h == -1, h, h & 0x7FFF))
     o, n = lay["hsz"]
     w[o:o + n] = 0
     return w
