@@ -232,3 +232,137 @@ class GameStream:
         return np.stack([uniform(s, F_GAME_MOVE + 0, k, e, 1, V), uniform(s, F_GAME_MOVE + 1, k, e, 1, V),
                          uniform(s, F_GAME_MOVE + 2, k, e, 0, S), uniform(s, F_GAME_MOVE + 3, k, e, 0, S)],
                         1).astype(np.int32)
+
+
+# ---- the same streams generated by torch, on the device (or the CPU) ----
+#
+# Bit for bit the numpy generator above: SplitMix64 in int64 arithmetic (which
+# wraps like uint64 for +, * and ^), logical shifts by masking, unsigned modulo
+# from the halved value, unsigned order for the geometric thresholds by flipping
+# the sign bit, and float64 +,-,*,/ (IEEE, correctly rounded) for the normal
+# draws. Used where generating on the host would dominate (large market counts);
+# tests/test_workloads_torch.py checks it against the numpy streams.
+
+def _i64(u: int) -> int:
+    """The int64 with the bits of uint64 u."""
+    u &= (1 << 64) - 1
+    return u - (1 << 64) if u >= (1 << 63) else u
+
+
+_T_GOLDEN, _T_C1, _T_C2 = _i64(0x9E3779B97F4A7C15), _i64(0xBF58476D1CE4E5B9), _i64(0x94D049BB133111EB)
+_T_SIGN = _i64(1 << 63)
+
+
+def _lsr(z, k: int):
+    return (z >> k) & ((1 << (64 - k)) - 1)
+
+
+def t_splitmix64(x):
+    z = x + _T_GOLDEN
+    z = (z ^ _lsr(z, 30)) * _T_C1
+    z = (z ^ _lsr(z, 27)) * _T_C2
+    return z ^ _lsr(z, 31)
+
+
+def t_draws(seed: int, field: int, step: int, markets):
+    """int64 tensor with the bits of draws(seed, field, step, markets)."""
+    if not (0 <= seed < 256 and 0 <= field < 256 and 0 <= step < (1 << 24)):
+        raise ValueError("seed/field/step out of the counter layout")
+    return t_splitmix64(markets | _i64((seed << 56) | (field << 48) | (step << 24)))
+
+
+def t_umod(h, n: int):
+    """Unsigned h mod n for int64 h holding uint64 bits (n < 2^62)."""
+    return ((_lsr(h, 1) % n) * 2 + (h & 1)) % n
+
+
+def t_uniform(seed, field, step, markets, lo: int, hi: int):
+    import torch
+    return (lo + t_umod(t_draws(seed, field, step, markets), hi - lo + 1)).to(torch.int32)
+
+
+def t_geometric(seed, field, step, markets, thresholds=_GEOM_03_50):
+    import torch
+    th = torch.tensor([_i64(int(v)) ^ _T_SIGN for v in thresholds], dtype=torch.int64,
+                      device=markets.device)
+    h = t_draws(seed, field, step, markets) ^ _T_SIGN
+    return (1 + torch.searchsorted(th, h, right=True)).to(torch.int32)
+
+
+def t_normal_irwin_hall(seed, field0, step, markets, mean: float, sd: float):
+    import torch
+    acc = torch.zeros_like(markets)
+    for k in range(16):
+        acc += _lsr(t_draws(seed, field0 + k, step, markets), 48)
+    mu = 16 * 32767.5
+    sigma = (16 * (65536.0 ** 2 - 1) / 12.0) ** 0.5
+    z = (acc.to(torch.float64) - mu) / sigma
+    return torch.floor(mean + sd * z + 0.5).to(torch.int64)
+
+
+class DeviceQuoteStream:
+    """QuoteStream's per-step inputs as int32 tensors on `device` (config 3's
+    random-walk mid lives there too, so steps come in order from 0)."""
+
+    def __init__(self, cfg: Config, markets=None, seed: int = 0, device="cuda"):
+        import torch
+        self.cfg, self.seed = cfg, seed
+        if markets is None:
+            self.markets = torch.arange(cfg.M, dtype=torch.int64, device=device)
+        else:
+            self.markets = torch.as_tensor(np.asarray(markets, np.int64)).to(device)
+        self._mid = torch.full(self.markets.shape, 64, dtype=torch.int64, device=self.markets.device)
+        self._next_step = 0
+
+    def step(self, t: int):
+        import torch
+        c, s, mk = self.cfg, self.seed, self.markets
+        if c.index == 1:
+            bid = t_uniform(s, F_BID_PX, t, mk, 0, 63)
+            ask = torch.clamp(bid.to(torch.int64) + t_uniform(s, F_ASK_PX, t, mk, 1, 63), max=127).to(torch.int32)
+            bsz = t_uniform(s, F_BID_SZ, t, mk, 1, 10)
+            asz = t_uniform(s, F_ASK_SZ, t, mk, 1, 10)
+            cust = torch.full(mk.shape, t % 16, dtype=torch.int32, device=mk.device)
+        elif c.index == 2:
+            bid = t_uniform(s, F_BID_PX, t, mk, 0, 127)
+            ask = t_uniform(s, F_ASK_PX, t, mk, 0, 127)
+            bsz = t_uniform(s, F_BID_SZ, t, mk, 1, 10)
+            asz = t_uniform(s, F_ASK_SZ, t, mk, 1, 10)
+            cust = t_uniform(s, F_CUST, t, mk, 0, 15)
+        elif c.index == 3:
+            if t != self._next_step:
+                raise ValueError("config 3 steps must be generated in order")
+            self._mid = torch.clamp(self._mid + t_uniform(s, F_MID, t, mk, -3, 3), 0, 127)
+            spread = t_uniform(s, F_SPREAD, t, mk, 0, 8).to(torch.int64)
+            b = torch.clamp(self._mid - spread // 2, 0, 127)
+            bid = b.to(torch.int32)
+            ask = torch.clamp(b + spread, 0, 127).to(torch.int32)
+            bsz = t_geometric(s, F_BID_SZ, t, mk)
+            asz = t_geometric(s, F_ASK_SZ, t, mk)
+            cust = t_uniform(s, F_CUST, t, mk, 0, 15)
+        elif c.index == 4:
+            bid = torch.clamp(t_normal_irwin_hall(s, F_NORMAL_BASE, t, mk, 256.0, 40.0), 0, 511).to(torch.int32)
+            ask = torch.clamp(t_normal_irwin_hall(s, F_NORMAL_BASE + 16, t, mk, 256.0, 40.0), 0, 511).to(torch.int32)
+            bsz = t_uniform(s, F_BID_SZ, t, mk, 1, 100)
+            asz = t_uniform(s, F_ASK_SZ, t, mk, 1, 100)
+            cust = t_uniform(s, F_CUST, t, mk, 0, 63)
+        else:
+            raise ValueError(f"no generator for config {c.index}")
+        self._next_step = t + 1
+        return bid, bsz, ask, asz, cust
+
+    def steps(self, t0: int, t1: int):
+        """Five int32 [t1 - t0, M] tensors, row k = step t0 + k."""
+        import torch
+        rows = [self.step(t) for t in range(t0, t1)]
+        return tuple(torch.stack([r[i] for r in rows]) for i in range(5))
+
+
+def t_game_move(cfg: GameConfig, k: int, envs, seed: int = 0):
+    """GameStream.move(k) as an int32 [N, 4] tensor on envs' device."""
+    import torch
+    V, S = cfg.max_contract_value, cfg.max_contracts_per_trade
+    return torch.stack([t_uniform(seed, F_GAME_MOVE + 0, k, envs, 1, V),
+                        t_uniform(seed, F_GAME_MOVE + 1, k, envs, 1, V),
+                        t_uniform(seed, F_GAME_MOVE + 2, k, envs, 0, S),
+                        t_uniform(seed, F_GAME_MOVE + 3, k, envs, 0, S)], 1).contiguous()

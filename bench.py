@@ -3,9 +3,14 @@
 
 A *step* is one ``add_two_sided_quotes`` over all markets (plus ``get_bbos`` when
 the config asks for it every step), i.e. one lock-step batch of two-sided quotes
-through the hot path. Inputs are generated on the host by the deterministic
-counter-based generator (astra_cuda.workloads), uploaded, and resident in HBM
-before timing starts.
+through the hot path. Inputs come from the deterministic counter-based generator
+(astra_cuda.workloads), run on the device; the steps from the warm-up on are
+generated up front and resident in HBM before timing starts.
+
+The default run (config 3, the headline) also measures configs 2, 4 and 5 of
+BASELINE.json, each over the end of its own run with the same window rule, and
+reports them under "configs". ``--sweep 1000,10000,...`` instead prints
+quote-matches/s at config 3's shape for each market count.
 
 The timed window is the END of the config's run: a config defines a run of
 ``steps`` steps (config 3: 1,000, whose order ring wraps at step 512 and evicts
@@ -30,7 +35,9 @@ pre-timed state, so they see exactly the same work):
      headline as value_rows_layout;
   S  the timed steps as ONE launch of the multi-step kernel
      (add_two_sided_quotes_steps, not in the reference; every step's BBOs kept),
-     reported beside the headline under "multistep".
+     reported beside the headline under "multistep";
+  G  the timed steps captured in one HIP graph through the drop-in API and
+     replayed once (the TID counter is in device memory), under "graph_replay".
 Then the CPU baseline: the oracle (a C port of the reference algorithm) on a
 bounded subset of the same markets, replaying the same pre-roll and warm-up
 untimed and timing the same window, on all host threads and on 1 thread.
@@ -77,9 +84,16 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the all-thread oracle leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--phases", default="ABCDRS",
+    ap.add_argument("--cpu-seconds-more", type=float, default=5.0,
+                    help="target CPU time of the oracle leg of each of configs 2, 4, 5 beside the headline")
+    ap.add_argument("--no-more-configs", action="store_true",
+                    help="with config 3: do not also run configs 2, 4 and 5 (reported under \"configs\")")
+    ap.add_argument("--sweep", default="",
+                    help="comma-separated market counts: quote-matches/s at config 3's shape for each "
+                         "(one JSON line with the points; e.g. 1000,10000,30000,100000,300000,1048576,4194304)")
+    ap.add_argument("--phases", default="ABCDRSG",
                     help="phases to run (A is always run; B latency, C events, D work counts, "
-                         "R row layout, S multi-step)")
+                         "R row layout, S multi-step, G graph replay)")
     ap.add_argument("--scatter-calibration", action="store_true",
                     help="only time scattered 4-byte writes, reads and atomic adds into a 1 GiB "
                          "buffer (the rate of scattered memory requests the device sustains)")
@@ -168,19 +182,42 @@ def main():
         return copy_calibration()
     if args.scatter_calibration:
         return scatter_calibration()
-
+    if args.sweep:
+        return bench_sweep(args)
     if args.config == 5:
-        return bench_game(args)
+        print(json.dumps(bench_game(args)), flush=True)
+        return
     if args.config == 6:
         return bench_game_reference(args)
+    result = bench_market(args, args.config)
+    if args.config == 3 and not args.markets and not args.no_more_configs:
+        result["configs"] = more_configs(args)
+    print(json.dumps(result), flush=True)
 
+
+def more_configs(args):
+    """Configs 2, 4 and 5 of BASELINE.json, each over the end of its own run (the
+    same --warmup / --steps window rule as the headline), reported beside it."""
+    import torch
+    out = {}
+    for idx in (2, 4, 5):
+        torch.cuda.empty_cache()
+        log(f"---- config {idx} ----")
+        out[f"config{idx}"] = bench_game(args, secondary=True) if idx == 5 else \
+            bench_market(args, idx, secondary=True)
+    return out
+
+
+def bench_market(args, cfg_index: int, secondary: bool = False, markets: int = 0):
+    """One VecMarket config over the timed window of its run; returns the result
+    dict (the headline's JSON line, or an entry of its "configs")."""
     import numpy as np
     import torch
     from astra_cuda import order_matching as aom
-    from astra_cuda.workloads import CONFIGS, QuoteStream
+    from astra_cuda.workloads import CONFIGS, DeviceQuoteStream
 
-    cfg = CONFIGS[args.config]
-    M = args.markets or cfg.M
+    cfg = CONFIGS[cfg_index]
+    M = markets or args.markets or cfg.M
     W, K = args.warmup, args.steps
     S = pre_roll(args, cfg.steps)
     T0 = S + W          # first timed step
@@ -188,55 +225,55 @@ def main():
     bbo = cfg.bbo_every_step and not args.no_bbo
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    phases = set(args.phases.upper()) | {"A"}
+    if secondary:
+        phases -= {"R", "S"}
 
-    # ---- inputs: generated on the host, resident in HBM before timing ----
+    # ---- inputs: the counter-based generator on the device; the steps from the
+    # warm-up on are generated up front and resident in HBM before timing, the
+    # pre-roll's step by step ----
     t0 = time.perf_counter()
-    qs = QuoteStream(cfg, np.arange(M))
-    host = qs.steps(0, T)
-    log(f"generated config {cfg.index} inputs: {T} steps x {M} markets in {time.perf_counter() - t0:.1f}s; "
-        f"timed steps [{T0}, {T})")
-    dev_in = [torch.from_numpy(a).to(dev) for a in host]
-    rows = [tuple(x[t] for x in dev_in) for t in range(T)]
-    torch.cuda.synchronize()
-
+    dq = DeviceQuoteStream(cfg, None if M == cfg.M else np.arange(M), device=dev)
     shape = dict(num_markets=M, max_price_levels=cfg.L, max_active_orders_per_market=cfg.O,
                  max_active_fills_per_market=cfg.F, num_customers=cfg.C)
     market = aom.VecMarket(**shape, allow_extended_shapes=cfg.extended)
     fills = market.new_fill_batch()
     bbos = market.new_bbo_batch()
 
-    def step(mk, t):
-        mk.add_two_sided_quotes(*rows[t], fills)
+    def step(mk, q):
+        mk.add_two_sided_quotes(*q, fills)
         if bbo:
             mk.get_bbos(bbos)
 
-    for t in range(T0):
-        step(market, t)
+    for t in range(S):
+        step(market, dq.step(t))
+    dev_in = list(dq.steps(S, T))
+    rows = {t: tuple(x[t - S] for x in dev_in) for t in range(S, T)}
+    for t in range(S, T0):
+        step(market, rows[t])
     torch.cuda.synchronize()
-    phases = set(args.phases.upper()) | {"A"}
-    # state at the start of the timed steps, for the replays B, C and D
-    snaps = [market.clone() if p in phases else None for p in "BCDRS"]
+    log(f"config {cfg.index}: {M} markets, pre-roll ({S} steps, inputs generated on the device) and "
+        f"warm-up ({W} steps) in {time.perf_counter() - t0:.1f}s; timing steps [{T0}, {T})")
+    # state at the start of the timed steps, for the replays B, C, D, R, S and G
+    snaps = {p: market.clone() for p in "BCDRSG" if p in phases}
     torch.cuda.synchronize()
-    log(f"pre-roll ({S} steps) and warm-up ({W} steps) done; timing {K} steps")
 
     # ---- A: throughput (the headline) ----
     torch.cuda.synchronize()
     a0 = time.perf_counter()
     for t in range(T0, T):
-        step(market, t)
+        step(market, rows[t])
     torch.cuda.synchronize()
     wall = time.perf_counter() - a0
     log(f"A: {K} steps in {wall * 1e3:.2f} ms")
 
     # ---- B: per-step latency (stream synced every step) ----
     nlat = min(K, args.latency_steps) if "B" in phases else 0
-    lat = [float("nan")]
-    if nlat:
-        lat = []
+    lat = [] if nlat else [float("nan")]
     for t in range(T0, T0 + nlat):
         torch.cuda.synchronize()
         h0 = time.perf_counter()
-        step(snaps[0], t)
+        step(snaps["B"], rows[t])
         torch.cuda.synchronize()
         lat.append(time.perf_counter() - h0)
     lat_ms = np.array(lat) * 1e3
@@ -244,45 +281,44 @@ def main():
     # ---- C: device time per kernel (HIP events on the launch stream) ----
     # The matching kernel of the K timed steps, replayed back to back (get_bbos
     # reads state only, so leaving it out changes no step), then K get_bbos.
-    qm_ms = np.array([wall / K * 1e3])
-    bbo_ms = np.zeros(1)
+    qm_ms, bbo_ms = wall / K * 1e3, 0.0
     if "C" in phases:
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         torch.cuda.synchronize()
         ev[0].record()
         for t in range(T0, T):
-            snaps[1].add_two_sided_quotes(*rows[t], fills)
+            snaps["C"].add_two_sided_quotes(*rows[t], fills)
         ev[1].record()
         if bbo:
             for t in range(T0, T):
-                snaps[1].get_bbos(bbos)
+                snaps["C"].get_bbos(bbos)
         ev[2].record()
         torch.cuda.synchronize()
-        qm_ms = np.array([ev[0].elapsed_time(ev[1]) / K])
+        qm_ms = ev[0].elapsed_time(ev[1]) / K
         if bbo:
-            bbo_ms = np.array([ev[1].elapsed_time(ev[2]) / K])
+            bbo_ms = ev[1].elapsed_time(ev[2]) / K
 
     # ---- D: exact work counts for the algorithmic bytes ----
     counters = torch.zeros(10, dtype=torch.int64, device=dev)
     if "D" in phases:
-        snaps[2]._set_stats(counters)
+        snaps["D"]._set_stats(counters)
         for t in range(T0, T):
-            snaps[2].add_two_sided_quotes(*rows[t], fills)
+            snaps["D"].add_two_sided_quotes(*rows[t], fills)
         torch.cuda.synchronize()
-        snaps[2]._set_stats(None)
+        snaps["D"]._set_stats(None)
     (n_ins, n_fill, n_empty, n_ovf, n_ff, n_pass, n_staged, n_cross, n_zruns,
      n_zrows) = (int(x) for x in counters.cpu().tolist())
 
     # ---- R: the same steps with the row layout of the FillBatch ----
     wall_rows = None
     if "R" in phases:
-        rfills = snaps[3].new_fill_batch(layout="rows")
+        rfills = snaps["R"].new_fill_batch(layout="rows")
         torch.cuda.synchronize()
         r0 = time.perf_counter()
         for t in range(T0, T):
-            snaps[3].add_two_sided_quotes(*rows[t], rfills)
+            snaps["R"].add_two_sided_quotes(*rows[t], rfills)
             if bbo:
-                snaps[3].get_bbos(bbos)
+                snaps["R"].get_bbos(bbos)
         torch.cuda.synchronize()
         wall_rows = time.perf_counter() - r0
         log(f"R: {K} steps in {wall_rows * 1e3:.2f} ms with the row layout")
@@ -291,21 +327,21 @@ def main():
     multistep = None
     if "S" in phases:
         step_bbos = torch.empty((4, K, M), dtype=torch.int32, device=dev) if bbo else None
-        ins = [x[T0:T] for x in dev_in]
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ins = [x[T0 - S:T - S] for x in dev_in]
+        sev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
 
         def one_launch(mk, layout):
             sfills = mk.new_fill_batch(layout)
             torch.cuda.synchronize()
             s0 = time.perf_counter()
-            ev[0].record()
+            sev[0].record()
             mk.add_two_sided_quotes_steps(*ins, sfills, step_bbos=step_bbos)
-            ev[1].record()
+            sev[1].record()
             torch.cuda.synchronize()
-            return time.perf_counter() - s0, ev[0].elapsed_time(ev[1]) / K
+            return time.perf_counter() - s0, sev[0].elapsed_time(sev[1]) / K
 
-        mk_rows = snaps[4].clone()
-        wall_ms, dev_ms = one_launch(snaps[4], "columns")
+        mk_rows = snaps["S"].clone()
+        wall_ms, dev_ms = one_launch(snaps["S"], "columns")
         wall_ms_rows, _ = one_launch(mk_rows, "rows")
         del mk_rows
         multistep = {"value": M * K / wall_ms, "ms_per_step": wall_ms / K * 1e3,
@@ -313,13 +349,37 @@ def main():
                      "value_rows_layout": M * K / wall_ms_rows,
                      "kernel": "quote_match_kernel (multi-step)"}
         log(f"S: {K} steps in one launch, {wall_ms * 1e3:.2f} ms ({wall_ms_rows * 1e3:.2f} ms with rows)")
+
+    # ---- G: the same K steps captured in one HIP graph (add_two_sided_quotes +
+    # get_bbos per step, through the drop-in API) and replayed once ----
+    graph = None
+    if "G" in phases:
+        gm = snaps["G"]
+        gfills, gbbos = gm.new_fill_batch(), gm.new_bbo_batch()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for t in range(T0, T):
+                gm.add_two_sided_quotes(*rows[t], gfills)
+                if bbo:
+                    gm.get_bbos(gbbos)
+        torch.cuda.synchronize()
+        g0 = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        gwall = time.perf_counter() - g0
+        del g
+        graph = {"value": M * K / gwall, "ms_per_step": gwall / K * 1e3, "steps_per_graph": K,
+                 "note": "the timed steps captured once (torch.cuda.graph) and replayed once; the "
+                         "TID counter lives in device memory, so a replay advances it"}
+        log(f"G: {K} steps as one graph replay in {gwall * 1e3:.2f} ms")
     log(f"work over {K} steps: inserts {n_ins}, fill rows {n_fill}, emptied {n_empty}, overflow {n_ovf}")
 
     # algorithmic bytes (per launch of the matching kernel): quotes in 20 B + fill_counts 4 B
     # per market; 32 B per accepted insert; 109 B per fill row; 8 B per emptied level.
     qm_bytes = (24.0 * M * K + 32.0 * n_ins + 109.0 * n_fill + 8.0 * n_empty) / K
     bbo_bytes = 24.0 * M  # 16 B out + 2 head-size reads of 4 B
-    qm_avg_s = float(qm_ms.mean()) * 1e-3
+    qm_avg_s = qm_ms * 1e-3
     achieved = qm_bytes / qm_avg_s / 1e9
 
     traffic, traffic_src = measured_traffic(cfg, M, bbo, (T0, T))
@@ -362,10 +422,12 @@ def main():
         "market_steps_per_s": K / wall,
         "value_rows_layout": (M * K / wall_rows) if wall_rows else None,
         "multistep": multistep,
+        "graph_replay": graph,
         "p50_step_latency_ms": float(np.percentile(lat_ms, 50)),
         "p99_step_latency_ms": float(np.percentile(lat_ms, 99)),
         "max_step_latency_ms": float(lat_ms.max()),
-        "device_ms_per_step": {"quote_match": float(qm_ms.mean()), "get_bbos": float(bbo_ms.mean())},
+        "binding": "ctypes (astra_cuda.order_matching)",
+        "device_ms_per_step": {"quote_match": float(qm_ms), "get_bbos": float(bbo_ms)},
         "work_per_step": {"inserts": n_ins / K, "fill_rows": n_fill / K, "levels_emptied": n_empty / K,
                           "overflow_markets": n_ovf / K, "crossing_markets": n_cross / K,
                           "loop_passes": n_pass / K, "staged_markets": n_staged / K,
@@ -387,14 +449,89 @@ def main():
             "scattered_requests": requests,
         },
     }
+    if secondary:
+        for k in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline", "dtype", "data"):
+            result.pop(k)
 
     # ---- CPU baseline: the oracle on a bounded subset of the same workload ----
+    del snaps, market, fills, bbos, dev_in, rows
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args, cfg, host, M, T0, K, bbo)
-    print(json.dumps(result), flush=True)
+        result["cpu_baseline"] = cpu_baseline(args, cfg, M, T0, K, bbo,
+                                              args.cpu_seconds_more if secondary else args.cpu_seconds)
+    return result
 
 
-def bench_game(args):
+def bench_sweep(args):
+    """Quote-matches/s over market counts at config 3's shape (the reference's
+    benchmark sweeps its market count the same way, benchmark_market.cc:256-268).
+    Each point runs the same timed window as the headline (steps 980-999 with the
+    driver's --steps 20 --warmup 5): A on the market itself; then on the same market
+    the work counts of the next K steps (D) and the matching kernel's device time
+    over the K steps after those (C), so that no copy of the book is needed at 4M
+    markets (the book and the FillBatch take 183 GiB there). The three windows lie
+    in the eviction regime of config 3 (the order ring wraps at step 512)."""
+    import numpy as np
+    import torch
+    from astra_cuda import order_matching as aom
+    from astra_cuda.workloads import CONFIGS, DeviceQuoteStream
+
+    cfg = CONFIGS[3]
+    W, K = args.warmup, args.steps
+    S = pre_roll(args, cfg.steps)
+    T0, T = S + W, S + W + K
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    points = []
+    for M in [int(x) for x in args.sweep.split(",")]:
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        dq = DeviceQuoteStream(cfg, np.arange(M), device=dev)
+        market = aom.VecMarket(M, cfg.L, cfg.O, cfg.F, cfg.C)
+        fills, bbos = market.new_fill_batch(), market.new_bbo_batch()
+
+        def step(q):
+            market.add_two_sided_quotes(*q, fills)
+            market.get_bbos(bbos)
+
+        for t in range(T0):
+            step(dq.step(t))
+        window = [dq.step(t) for t in range(T0, T + 2 * K)]
+        torch.cuda.synchronize()
+        a0 = time.perf_counter()
+        for q in window[:K]:
+            step(q)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - a0
+        counters = torch.zeros(10, dtype=torch.int64, device=dev)
+        market._set_stats(counters)
+        for q in window[K:2 * K]:
+            market.add_two_sided_quotes(*q, fills)
+        torch.cuda.synchronize()
+        market._set_stats(None)
+        n_ins, n_fill, n_empty = (int(x) for x in counters.cpu().tolist()[:3])
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        for q in window[2 * K:]:
+            market.add_two_sided_quotes(*q, fills)
+        ev[1].record()
+        torch.cuda.synchronize()
+        qm_ms = ev[0].elapsed_time(ev[1]) / K
+        qm_bytes = (24.0 * M * K + 32.0 * n_ins + 109.0 * n_fill + 8.0 * n_empty) / K
+        frac = qm_bytes / (qm_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+        pt = {"markets": M, "value": M * K / wall, "ms_per_step": wall / K * 1e3,
+              "quote_match_device_ms": qm_ms, "roofline_frac": frac,
+              "algorithmic_bytes_per_launch": qm_bytes,
+              "windows": {"A": [T0, T], "D": [T, T + K], "C": [T + K, T + 2 * K]}}
+        points.append(pt)
+        log(f"sweep {M} markets: {pt['value']:.3e} quote-matches/s, {pt['ms_per_step']:.3f} ms/step, "
+            f"kernel {qm_ms * 1e3:.1f} us, frac {frac:.4f} ({time.perf_counter() - t0:.1f}s)")
+        del market, fills, bbos, window, dq
+    print(json.dumps({"metric": "quote-matches/sec over market counts (config 3 shape)", "unit": "quote-matches/s",
+                      "sweep": points, "config": {"workload": "config3_stress_100k shape", "timed_steps": [T0, T]}}),
+          flush=True)
+
+
+def bench_game(args, secondary: bool = False):
     """Config 5: one trading move of every env of the high-low game per step
     (HighLowTradingState::ApplyPlayerTrading: AddTwoSidedQuotes, GetBBOs,
     UpdateLastPrices and the per-player rewards and telemetry). The chance moves
@@ -436,7 +573,7 @@ def bench_game(args):
     for k in range(T0):
         state.apply_action(moves[k])
     torch.cuda.synchronize()
-    snaps = [state.clone() for _ in range(4)]
+    snaps = [state.clone() for _ in range(5)]
     torch.cuda.synchronize()
     log(f"pre-roll ({S} moves) and warm-up ({W} moves) done; timing {K} moves")
 
@@ -483,6 +620,23 @@ def bench_game(args):
     torch.cuda.synchronize()
     st.market._set_stats(None)
     n_ins, n_fill, n_empty = (int(x) for x in counters.cpu().tolist()[:3])
+    # G: the unchecked moves captured in one HIP graph and replayed once (the
+    # move's kernel reads the TID counter from device memory; the acting player
+    # and move number are kernel arguments, which the capture records in order)
+    st = snaps[4]
+    st.set_check_moves(False)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for k in range(T0, T0 + K):
+            st.apply_action(moves[k])
+    torch.cuda.synchronize()
+    g0 = time.perf_counter()
+    gr.replay()
+    torch.cuda.synchronize()
+    gwall = time.perf_counter() - g0
+    del gr
+    log(f"G: {K} unchecked moves as one graph replay in {gwall * 1e3:.2f} ms")
     # algorithmic bytes per move: the matching kernel's (24 B per env + 32 per insert +
     # 109 per fill row + 8 per emptied level) plus the game's work fused into it:
     # reads of the move 16 B, contract value 4 B, last price 4 B and per player the
@@ -517,6 +671,8 @@ def bench_game(args):
         "market_steps_per_s": K / wall,
         "value_unchecked": N * K / wall_unchecked,
         "ms_per_step_unchecked": wall_unchecked / K * 1e3,
+        "graph_replay": {"value": N * K / gwall, "ms_per_step": gwall / K * 1e3, "steps_per_graph": K,
+                         "note": "the timed moves, unchecked, captured once and replayed once"},
         "p50_step_latency_ms": float(np.percentile(lat_ms, 50)),
         "p99_step_latency_ms": float(np.percentile(lat_ms, 99)),
         "device_ms_per_step": {"fused_move_kernel": step_ms},
@@ -527,9 +683,14 @@ def bench_game(args):
             "traffic": traffic, "traffic_source": traffic_src, "algorithmic_bytes_per_launch": step_bytes,
         },
     }
+    if secondary:
+        for k in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline", "dtype", "data"):
+            result.pop(k)
+    del snaps, state, st, moves
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = game_cpu_baseline(args, cfg, chance, host_moves, N, T0, K)
-    print(json.dumps(result), flush=True)
+        result["cpu_baseline"] = game_cpu_baseline(args, cfg, chance, host_moves, N, T0, K,
+                                                   args.cpu_seconds_more if secondary else args.cpu_seconds)
+    return result
 
 
 # src/tests/README.md:142,144-145: the reference's best game figure, RTX 5090
@@ -630,7 +791,7 @@ def bench_game_reference(args):
     print(json.dumps(result), flush=True)
 
 
-def game_cpu_baseline(args, cfg, chance, host_moves, N, T0, K):
+def game_cpu_baseline(args, cfg, chance, host_moves, N, T0, K, seconds):
     """The game oracle (numpy state operations over the C market oracle, one
     thread) on the first envs of the same stream: the same untimed moves [0, T0),
     then the timed moves [T0, T0 + K)."""
@@ -655,7 +816,7 @@ def game_cpu_baseline(args, cfg, chance, host_moves, N, T0, K):
     rate = run(n0, 0, min(T0 + K, 50))
     # envs such that the untimed moves and the timed window together take about
     # cpu_seconds
-    n = int(min(N, max(500, rate * args.cpu_seconds / (T0 + K))))
+    n = int(min(N, max(500, rate * seconds / (T0 + K))))
     log(f"CPU leg: {n} envs, {T0} untimed + {K} timed moves")
     v = run(n, T0, K)
     return {"value": v, "unit": "quote-matches/s", "cores": 1, "kind": "port",
@@ -731,18 +892,21 @@ def game_traffic(cfg, N, window):
                            "quote_match_kernel<2, false, true, false, true", window)
 
 
-def cpu_baseline(args, cfg, host, M, T0, K, bbo):
-    """The C oracle on markets [0, mc) of the same stream: steps [0, T0) untimed,
-    then the timed window [T0, T0 + K) on all host threads; then, from a copy of
-    the state at T0, the first steps of the window on one thread."""
+def cpu_baseline(args, cfg, M, T0, K, bbo, seconds):
+    """The C oracle on markets [0, mc) of the same stream (generated on the host by
+    the numpy generator, which the device generator reproduces bit for bit):
+    steps [0, T0) untimed, then the timed window [T0, T0 + K) on all host threads;
+    then, from a copy of the state at T0, the first steps of the window on one
+    thread. mc is sized so that the whole leg takes about `seconds`."""
     import numpy as np
+    from astra_cuda.workloads import QuoteStream
     from oracle.oracle import OracleMarket
 
     model, avail = cpu_info()
     nthreads = max(1, avail)
 
-    def sliced(mc):
-        return [np.ascontiguousarray(a[:, :mc]) for a in host]
+    def sliced(mc, t1=None):
+        return QuoteStream(cfg, np.arange(mc)).steps(0, T0 + K if t1 is None else t1)
 
     def steps(o, f, b, sl, t0, t1, threads, with_bbo):
         for t in range(t0, t1):
@@ -751,16 +915,17 @@ def cpu_baseline(args, cfg, host, M, T0, K, bbo):
                 o.get_bbos(b, nthreads=threads)
 
     # calibrate on a small sample, then size the sample so that the untimed steps
-    # and the window together take about cpu_seconds on all threads
+    # and the window together take about `seconds` on all threads
     mc0 = min(M, 2000)
     o = OracleMarket(mc0, cfg.L, cfg.O, cfg.F, cfg.C)
     f, b = o.new_fill_batch(), o.new_bbo_batch()
     n0 = min(T0 + K, 50)
+    sl0 = sliced(mc0, n0)
     c0 = time.perf_counter()
-    steps(o, f, b, sliced(mc0), 0, n0, nthreads, bbo)
+    steps(o, f, b, sl0, 0, n0, nthreads, bbo)
     rate = mc0 * n0 / (time.perf_counter() - c0)
-    del o, f, b
-    mc = int(min(M, max(1000, rate * args.cpu_seconds / (T0 + K))))
+    del o, f, b, sl0
+    mc = int(min(M, max(1000, rate * seconds / (T0 + K))))
     log(f"CPU leg: {mc} markets, {T0} untimed + {K} timed steps on {nthreads} threads")
     sl = sliced(mc)
     o = OracleMarket(mc, cfg.L, cfg.O, cfg.F, cfg.C)
@@ -773,7 +938,7 @@ def cpu_baseline(args, cfg, host, M, T0, K, bbo):
     del o
     # one thread: window steps one at a time until a third of cpu_seconds is spent
     k1, spent = 0, 0.0
-    while k1 < K and spent < args.cpu_seconds / 3:
+    while k1 < K and spent < seconds / 3:
         c0 = time.perf_counter()
         steps(o1, f, b, sl, T0 + k1, T0 + k1 + 1, 1, bbo)
         spent += time.perf_counter() - c0
