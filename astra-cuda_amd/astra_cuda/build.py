@@ -44,6 +44,44 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the HIP engine cannot be built")
 
 
+BINDING_SRC = os.path.join(CSRC, "bindings.cpp")
+
+
+def binding_path() -> str:
+    import sysconfig
+    return os.path.join(PKG_DIR, "_C" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_binding(verbose: bool = False) -> str:
+    """Compile the pybind11 module astra_cuda._C (csrc/bindings.cpp, the reference's
+    market_bindings.cc surface over the C ABI) against torch's headers and libraries,
+    linked to libastra_market.so in the same directory. Always recompiles."""
+    import sysconfig
+    import torch
+    tdir = os.path.dirname(torch.__file__)
+    incs = [os.path.join(tdir, "include"), os.path.join(tdir, "include", "torch", "csrc", "api", "include"),
+            "/opt/rocm/include", sysconfig.get_paths()["include"], INCLUDE]
+    out = binding_path()
+    tmp = out + ".tmp"
+    cxx = os.environ.get("CXX", "g++")
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           *(f"-I{d}" for d in incs), BINDING_SRC,
+           f"-L{os.path.join(tdir, 'lib')}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+           "-ltorch_python", f"-L{PKG_DIR}", "-l:" + LIB_NAME,
+           # the engine library next to the module, and torch's libraries
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{os.path.join(tdir, 'lib')}", "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"{cxx} failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> str:
     """Compile the sources into the package directory. Always recompiles."""
     tmp = LIB_PATH + ".tmp"
@@ -59,3 +97,4 @@ def build(verbose: bool = False) -> str:
 
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    print(build_binding(verbose="-v" in sys.argv))

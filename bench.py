@@ -267,16 +267,42 @@ def bench_market(args, cfg_index: int, secondary: bool = False, markets: int = 0
     wall = time.perf_counter() - a0
     log(f"A: {K} steps in {wall * 1e3:.2f} ms")
 
-    # ---- B: per-step latency (stream synced every step) ----
+    # ---- B: per-step latency (stream synced every step) and the host time of the
+    # calls, through this package's binding and through the compiled one (a copy
+    # of the same book) ----
     nlat = min(K, args.latency_steps) if "B" in phases else 0
-    lat = [] if nlat else [float("nan")]
-    for t in range(T0, T0 + nlat):
-        torch.cuda.synchronize()
-        h0 = time.perf_counter()
-        step(snaps["B"], rows[t])
-        torch.cuda.synchronize()
-        lat.append(time.perf_counter() - h0)
-    lat_ms = np.array(lat) * 1e3
+    bindings = {}
+    lat_ms = np.array([float("nan")])
+    if nlat:
+        from astra_cuda._C import order_matching as com
+        cm = com.VecMarket(M, cfg.L, cfg.O, cfg.F, cfg.C) if not cfg.extended else None
+        if cm is not None:
+            cm._workspace.copy_(snaps["B"]._ws[:cm._workspace.numel()])
+            cfills, cbbos = cm.new_fill_batch(), cm.new_bbo_batch()
+        for name, mk in (("ctypes", snaps["B"]), ("compiled", cm)):
+            if mk is None:
+                continue
+            f_, b_ = (fills, bbos) if name == "ctypes" else (cfills, cbbos)
+            lat, host = [], []
+            for t in range(T0, T0 + nlat):
+                torch.cuda.synchronize()
+                h0 = time.perf_counter()
+                mk.add_two_sided_quotes(*rows[t], f_)
+                h1 = time.perf_counter()
+                if bbo:
+                    mk.get_bbos(b_)
+                torch.cuda.synchronize()
+                lat.append(time.perf_counter() - h0)
+                host.append(h1 - h0)
+            bindings[name] = {"p50_step_latency_ms": float(np.percentile(lat, 50) * 1e3),
+                              "p99_step_latency_ms": float(np.percentile(lat, 99) * 1e3),
+                              "host_us_per_add_two_sided_quotes_p50": float(np.percentile(host, 50) * 1e6)}
+            if name == "ctypes":
+                lat_ms = np.array(lat) * 1e3
+        del cm
+        log("B: " + ", ".join(f"{k} p50 {v['p50_step_latency_ms'] * 1e3:.1f} us (host "
+                              f"{v['host_us_per_add_two_sided_quotes_p50']:.1f} us per call)"
+                              for k, v in bindings.items()))
 
     # ---- C: device time per kernel (HIP events on the launch stream) ----
     # The matching kernel of the K timed steps, replayed back to back (get_bbos
@@ -427,6 +453,7 @@ def bench_market(args, cfg_index: int, secondary: bool = False, markets: int = 0
         "p99_step_latency_ms": float(np.percentile(lat_ms, 99)),
         "max_step_latency_ms": float(lat_ms.max()),
         "binding": "ctypes (astra_cuda.order_matching)",
+        "bindings": bindings or None,
         "device_ms_per_step": {"quote_match": float(qm_ms), "get_bbos": float(bbo_ms)},
         "work_per_step": {"inserts": n_ins / K, "fill_rows": n_fill / K, "levels_emptied": n_empty / K,
                           "overflow_markets": n_ovf / K, "crossing_markets": n_cross / K,

@@ -60,6 +60,18 @@ class GpuRowAdapter(GpuAdapter):
     layout = "rows"
 
 
+class GpuCompiledAdapter(GpuAdapter):
+    """KAT adapter over the compiled binding astra_cuda._C.order_matching (the
+    reference's pybind surface: reference caps, the per-field FillBatch)."""
+    layout = "compiled"
+
+    def __init__(self, shape):
+        from astra_cuda._C import order_matching as com
+        self.mk = com.VecMarket(shape["M"], shape["L"], shape["O"], shape["F"], shape["C"])
+        self.fills = self.mk.new_fill_batch()
+        self.bbo = self.mk.new_bbo_batch()
+
+
 def effective_counts(counts: np.ndarray, F: int) -> np.ndarray:
     """Number of fill rows written by the last call (F for an overflowed market)."""
     return np.where(counts < 0, F, counts)
@@ -152,14 +164,21 @@ def run_parity(M, L, O, F, C, steps, gen, *, bbo_every=1, full_every=0, last_eve
                per_wave=None, fill_rows=None, helpers=None, hand_lanes=None, hand_queue=None,
                helper_polls=None):
     """Drive GPU engine and oracle with the same inputs; compare after every step.
+    layout "columns" / "rows" picks the FillBatch layout of astra_cuda.order_matching;
+    "compiled" runs the compiled binding astra_cuda._C.order_matching instead.
 
     ``gen(t)`` returns (bid_px, bid_sz, ask_px, ask_sz, cust) int32 arrays of shape [M].
     Returns summary statistics (fill rows compared, overflows seen).
     """
     from oracle.oracle import OracleMarket
-    g = make_market(M, L, O, F, C, extended, stage_budget, per_wave, fill_rows, helpers, hand_lanes,
-                    hand_queue, helper_polls)
-    gf, gb = g.new_fill_batch(layout), g.new_bbo_batch()
+    if layout == "compiled":  # the compiled binding (reference caps, per-field FillBatch)
+        from astra_cuda._C import order_matching as com
+        g = com.VecMarket(M, L, O, F, C)
+        gf, gb = g.new_fill_batch(), g.new_bbo_batch()
+    else:
+        g = make_market(M, L, O, F, C, extended, stage_budget, per_wave, fill_rows, helpers, hand_lanes,
+                        hand_queue, helper_polls)
+        gf, gb = g.new_fill_batch(layout), g.new_bbo_batch()
     o = OracleMarket(M, L, O, F, C)
     of, ob = o.new_fill_batch(), o.new_bbo_batch()
     rows = overflows = 0

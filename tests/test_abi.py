@@ -104,3 +104,31 @@ def test_test_side_workspace_layout_matches_the_engine(shape):
     M, L, O, F, C = shape
     rc, n, _ = _ws(*shape, flags=1)
     assert rc == 0 and layout(M, L, O, C)["total"][1] == n
+
+
+def test_compiled_binding_has_the_reference_module_surface():
+    """astra_cuda._C.order_matching exposes what market_bindings.cc:14-73 binds: the
+    three classes, their tensor fields, the methods with the reference's keyword
+    names, and the six constants (import only: no device calls on the CPU)."""
+    from astra_cuda.build import binding_path, build_binding
+    if not os.path.exists(binding_path()):
+        build_binding()
+    from astra_cuda._C import order_matching as com
+    for f in ("best_bid_prices", "best_bid_sizes", "best_ask_prices", "best_ask_sizes"):
+        assert isinstance(getattr(com.BBOBatch, f), property)
+    for f in ("fill_prices", "fill_sizes", "fill_customer_ids", "fill_quoter_ids", "fill_is_sell_quote",
+              "fill_quote_sizes", "fill_tid", "fill_quote_tid", "fill_counts"):
+        assert isinstance(getattr(com.FillBatch, f), property)
+    for m in ("new_fill_batch", "new_bbo_batch", "add_two_sided_quotes", "get_bbos", "to_string",
+              "get_customer_portfolios"):
+        assert callable(getattr(com.VecMarket, m))
+    doc = com.VecMarket.__init__.__doc__
+    for kw in ("num_markets", "max_price_levels", "max_active_orders_per_market",
+               "max_active_fills_per_market"):
+        assert kw + ":" in doc, kw
+    for kw, default in (("num_customers", 16), ("device_id", 0), ("threads_per_block", 64)):
+        assert re.search(kw + r": [\w.]+ = " + str(default), doc), kw
+    assert "bid_px" in com.VecMarket.add_two_sided_quotes.__doc__ and "fills" in \
+        com.VecMarket.add_two_sided_quotes.__doc__
+    assert (com.MAX_MARKETS, com.PRICE_LEVELS, com.MAX_ACTIVE_ORDERS_PER_MARKET, com.MAX_ACTIVE_FILLS_PER_MARKET,
+            com.NULL_INDEX, com.MAX_CUSTOMERS) == (2048 * 2048, 128, 1024, 1024, -1, 1024)
