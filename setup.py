@@ -1,5 +1,6 @@
 """Wheel build of the astra_cuda package (astra-cuda_amd/astra_cuda): compiles
-libastra_market.so (the HIP engine, astra-cuda_amd/csrc) into the package
+libastra_market.so (the HIP engine, astra-cuda_amd/csrc) and the compiled binding
+astra_cuda._C (csrc/bindings.cpp, against the installed torch) into the package
 directory before the package files are collected.
 
     pip install --no-build-isolation .
@@ -18,8 +19,9 @@ class BuildPyWithEngine(build_py):
         path = os.path.join(HERE, "astra-cuda_amd", "astra_cuda", "build.py")
         spec = importlib.util.spec_from_file_location("astra_cuda_build", path)
         mod = importlib.util.module_from_spec(spec)
-        spec.loader.exec_module(mod)  # build.py imports only the standard library
-        print("built", mod.build(verbose=True))
+        spec.loader.exec_module(mod)  # build.py imports only the standard library (and torch
+        print("built", mod.build(verbose=True))  # for the binding)
+        print("built", mod.build_binding(verbose=True))
         super().run()
 
 
@@ -32,6 +34,6 @@ setup(
     install_requires=["numpy", "torch"],
     package_dir={"": "astra-cuda_amd"},
     packages=["astra_cuda"],
-    package_data={"astra_cuda": ["libastra_market.so"]},
+    package_data={"astra_cuda": ["libastra_market.so", "_C*.so"]},
     cmdclass={"build_py": BuildPyWithEngine},
 )
