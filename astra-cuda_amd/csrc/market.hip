@@ -44,6 +44,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #define ASTRA_SRC_NAME "market.hip"
@@ -638,6 +639,7 @@ struct GlobalBook {
 
 struct StagedBook {
   static constexpr bool kStaged = true;
+  static constexpr bool kLean = true;  // the loop's lean runs (cross_run, zero_levels)
   uint16_t *slv;  // the copy
   uint4 *srec;
   uint16_t *glv;  // the market's arrays in global memory
@@ -688,6 +690,15 @@ struct UniformStagedBook : StagedBook {
   }
   ASTRA_HD uint32_t word(int32_t p, int side) const { return uni(level_word(slv, p, side)); }
   ASTRA_HD uint32_t head(int32_t p, int side) const { return uni(level_head(slv, p, side)); }
+};
+
+// The same without the loop's lean runs (the game's move kernel: their code
+// costs it more registers than they save it time).
+struct UniformStagedBookPlain : UniformStagedBook {
+  static constexpr bool kLean = false;
+};
+struct StagedBookPlain : StagedBook {
+  static constexpr bool kLean = false;
 };
 
 template <int W>
@@ -1181,6 +1192,143 @@ ASTRA_HD bool zero_walk(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, 
   return ok;
 }
 
+// On a staged book, passes whose one head has positive size and whose other
+// head is an order of size 0 that is the last of its level (a consumed order
+// still linked after ring-slot reuse): each fills 0 against it and empties its
+// level (market.cu:196-273 with q = 0; the pop to the next level, :241-256 /
+// :258-273). Runs such passes back to back while the side's next level holds
+// such an order too and still crosses. Called at the top of a pass with both
+// records loaded (the side's head of that kind, the other head of positive
+// size, distinct heads, fills left); returns false when the budget or the sink
+// stopped it (state intact at the top of a pass), else true with the state at
+// the top of a pass.
+template <int SIDE, bool STATS, int W, class BookMem, class Sink>
+ASTRA_HD bool zero_levels(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, Sink &sink,
+                          const FillOut &out, int32_t budget, int32_t &passes) {
+  uint4 &w = SIDE == 0 ? s.brec : s.arec;
+  uint32_t &h = SIDE == 0 ? s.bh : s.ah;
+  int &p = SIDE == 0 ? s.bb : s.ba;
+  bool &have = SIDE == 0 ? s.have_b : s.have_a;
+  uint64_t(&m)[W] = SIDE == 0 ? s.bm : s.am;
+  const uint32_t other = SIDE == 0 ? s.ah : s.bh;
+  const int32_t L = c.L;
+  for (;;) {
+    s.last_px = sink.put_fill(out, c.pf, c.C, s.brec, s.arec, s.bh, s.ah, 0);
+    ++s.fc;
+    if (STATS) {
+      ++s.npass;
+      ++s.emptied;
+    }
+    bk.set_word(p, SIDE, 0xFFFFFFFFu);
+    mask_clear<W>(m, p);
+    p = SIDE == 0 ? mask_highest<W>(m) : mask_lowest<W>(m, L);
+    const bool live = SIDE == 0 ? p >= 0 : p < L;
+    const uint32_t nh = bk.head(live ? p : 0, SIDE);
+    h = live ? nh : kNull16;
+    have = false;
+    // the top of the next pass
+    if (!live || s.bb < s.ba || h >= (uint32_t)c.O) return true;
+    w = bk.record(h);
+    have = true;
+    if (h == other || (int32_t)w.x != 0 || rec_next(w) != kNull16 || s.fc >= c.F) return true;
+    if (passes++ >= budget || sink.full()) return false;
+  }
+}
+
+// On a staged book: passes of the crossing loop below run back to back while
+// both heads are distinct orders of positive size (market.cu:196-273 for that
+// case: the fill is the smaller size, both sizes drop by it, and a side whose
+// size is then 0 pops to the next order of its level or, at the end of the
+// level, to the next level). Size-0 heads are left to zero_walk and
+// zero_levels, repeating and aliased states to the loop below. A pass of the
+// loop below on a staged book costs ~1,600 cycles (one wavefront, one lane:
+// instruction issue, taken branches and LDS round trips one after another);
+// this run keeps its state in registers, reads both head records together
+// once per pass, and writes a surviving order's size and a level's new head
+// once, when the run ends or the level empties. Called at the top of a pass
+// with both records loaded and the book crossing; returns whether it made a
+// pass, and leaves every write in the book and the state at the top of a pass
+// (the loop's next pass reads both records again).
+template <int W, bool STATS, class BookMem, class Sink>
+ASTRA_HD bool cross_run(LoopState<W> &s, const MarketCtx &c, const BookMem &bk, Sink &sink,
+                        const FillOut &out, int32_t budget, int32_t &passes) {
+  const int32_t L = c.L;
+  const uint32_t O = (uint32_t)c.O;
+  bool any = false;
+  bool size_b = false, size_a = false;  // the head's size in the book is stale
+  bool head_b = false, head_a = false;  // the level's head word is stale
+  int32_t bsz = (int32_t)s.brec.x, asz = (int32_t)s.arec.x;
+  for (;;) {
+    if (s.bh == s.ah || bsz <= 0 || asz <= 0 || s.fc >= c.F) break;
+    const uint32_t nb = rec_next(s.brec), na = rec_next(s.arec);
+    if (any) {
+      if (passes >= budget || sink.full()) break;
+      ++passes;
+    }
+    any = true;
+    if (STATS) ++s.npass;
+    const int32_t qty = bsz < asz ? bsz : asz;
+    s.last_px = sink.put_fill(out, c.pf, c.C, s.brec, s.arec, s.bh, s.ah, qty);
+    ++s.fc;
+    bsz -= qty;  // both >= 0: no wrap
+    asz -= qty;
+    const bool pop_b = bsz == 0, pop_a = asz == 0;
+    size_b = !pop_b;  // (qty > 0: the size changed)
+    size_a = !pop_a;
+    s.brec.x = (uint32_t)bsz;
+    s.arec.x = (uint32_t)asz;
+    if (pop_b) {
+      bk.set_size(s.bh, 0);
+      if (nb == kNull16) {
+        bk.set_word(s.bb, 0, 0xFFFFFFFFu);
+        head_b = false;
+        mask_clear<W>(s.bm, s.bb);
+        if (STATS) ++s.emptied;
+        s.bb = mask_highest<W>(s.bm);
+        const uint32_t h = bk.head(s.bb >= 0 ? s.bb : 0, 0);
+        s.bh = s.bb >= 0 ? h : kNull16;
+      } else if (nb != s.bh) {
+        s.bh = nb;
+        head_b = true;
+      }
+      s.have_b = false;
+    }
+    if (pop_a) {
+      bk.set_size(s.ah, 0);
+      if (na == kNull16) {
+        bk.set_word(s.ba, 1, 0xFFFFFFFFu);
+        head_a = false;
+        mask_clear<W>(s.am, s.ba);
+        if (STATS) ++s.emptied;
+        s.ba = mask_lowest<W>(s.am, L);
+        const uint32_t h = bk.head(s.ba < L ? s.ba : 0, 1);
+        s.ah = s.ba < L ? h : kNull16;
+      } else if (na != s.ah) {
+        s.ah = na;
+        head_a = true;
+      }
+      s.have_a = false;
+    }
+    // the top of the next pass
+    if (s.bb < 0 || s.ba >= L || s.bb < s.ba || s.bh >= O || s.ah >= O) break;
+    // both records at once; a head that did not pop keeps its size (the book's
+    // copy may be stale) and its other fields (which nothing changes)
+    const uint4 rb = bk.record(s.bh), ra = bk.record(s.ah);
+    s.brec = rb;
+    s.arec = ra;
+    bsz = pop_b ? (int32_t)rb.x : bsz;
+    asz = pop_a ? (int32_t)ra.x : asz;
+    s.brec.x = (uint32_t)bsz;
+    s.arec.x = (uint32_t)asz;
+    s.have_b = s.have_a = true;
+  }
+  if (size_b) bk.set_size(s.bh, (int32_t)s.brec.x);
+  if (size_a) bk.set_size(s.ah, (int32_t)s.arec.x);
+  if (head_b) bk.set_head(s.bb, 0, s.bh);
+  if (head_a) bk.set_head(s.ba, 1, s.ah);
+  return any;
+}
+
 // match_orders_kernel's crossing loop (market.cu:145-274). Runs at most
 // `budget` passes and stops early when the sink is full, or (EARLY, in global
 // memory) before a zero-size walk of a lane left nearly alone
@@ -1274,6 +1422,19 @@ ASTRA_HD bool match_loop(LoopState<W> &s, const MarketCtx &c, const BookMem &bk,
         } else if ((int32_t)s.arec.x == 0 && (int32_t)s.brec.x > 0) {
           if (!zero_walk<1, STATS>(s, c, bk, sink, out, budget, passes)) return false;
         }
+      }
+      if constexpr (BookMem::kLean) {
+        if (s.bh != s.ah && s.fc < F) {
+          if ((int32_t)s.brec.x == 0 && rec_next(s.brec) == kNull16 && (int32_t)s.arec.x > 0) {
+            if (!zero_levels<0, STATS>(s, c, bk, sink, out, budget, passes)) return false;
+            continue;
+          }
+          if ((int32_t)s.arec.x == 0 && rec_next(s.arec) == kNull16 && (int32_t)s.brec.x > 0) {
+            if (!zero_levels<1, STATS>(s, c, bk, sink, out, budget, passes)) return false;
+            continue;
+          }
+        }
+        if (cross_run<W, STATS>(s, c, bk, sink, out, budget, passes)) continue;
       }
     }
     if (STATS) ++s.npass;
@@ -1678,7 +1839,7 @@ __device__ void finish_staged(const Book &b, const FillOut &out, int32_t *stage,
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  UniformStagedBook sb;
+  std::conditional_t<GAME, UniformStagedBookPlain, UniformStagedBook> sb;
   sb.slv = reinterpret_cast<uint16_t *>(slv);
   sb.srec = srec;
   sb.glv = reinterpret_cast<uint16_t *>(glv);
@@ -2111,7 +2272,11 @@ int launch_quote_match(const astra_market *h, const QuoteIn &in, const FillOut &
       }
       std::memcpy(srec.data(), c.rec, (size_t)h->O * 16);
       std::memcpy(slv.data(), c.lv, (size_t)h->L * 8);
-      const StagedBook sb{slv.data(), srec.data(), c.lv, c.rec};
+      std::conditional_t<GAME, StagedBookPlain, StagedBook> sb;
+      sb.slv = slv.data();
+      sb.srec = srec.data();
+      sb.glv = c.lv;
+      sb.grec = c.rec;
       RowBuffer rb{rows.data(), kStageRows, 0, sink.base};
       bool fin = false;
       while (!fin) {
