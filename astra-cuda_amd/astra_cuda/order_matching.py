@@ -531,16 +531,17 @@ class VecMarket:
     # -- introspection (not in the reference binding) -------------------------
 
     def _set_stats(self, counters) -> None:
-        """Diagnostic: accumulate per-call work counts into an int64 [10] device tensor
+        """Diagnostic: accumulate per-call work counts into an int64 [11] device tensor
         (inserts, fill rows, emptied levels, overflowed markets, fast-forwarded
         overflows, loop passes, staged markets, crossing markets, zero-size runs
-        listed on a staged book and their rows); None switches it off."""
+        listed on a staged book and their rows, best levels whose head size the
+        next get_bbos reads from the book); None switches it off."""
         if counters is None:
             _check(self._lib.astra_market_set_stats(self._h, None))
             return
-        if (counters.dtype != torch.int64 or counters.numel() < 10 or counters.device != self._device
+        if (counters.dtype != torch.int64 or counters.numel() < 11 or counters.device != self._device
                 or not counters.is_contiguous()):
-            _fatal("stats counters must be a contiguous int64 tensor of >= 10 elements on the engine's device")
+            _fatal("stats counters must be a contiguous int64 tensor of >= 11 elements on the engine's device")
         self._stats_ref = counters
         _check(self._lib.astra_market_set_stats(self._h, counters.data_ptr()))
 

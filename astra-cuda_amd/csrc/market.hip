@@ -153,7 +153,7 @@ struct Book {
   uint16_t *levels;           // [M][L][4] = {bid_head, bid_tail, ask_head, ask_tail}
   uint4 *records;             // [M][O] = {size, customer, tid, price | next << 16}
   int32_t *portfolios;        // [M][C][2] = {contracts, cash}
-  unsigned long long *stats;  // diagnostic counters [10] or nullptr
+  unsigned long long *stats;  // diagnostic counters [11] or nullptr
   int32_t M, L, O, F, C;
 };
 
@@ -1041,9 +1041,15 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
   const uint32_t bword = bid_ok ? bword_ld : 0u;
   const uint32_t aword = ask_ok ? aword_ld : 0u;
   uint4 hrb = make_uint4((uint32_t)bsz0, 0, 0, 0), hra = make_uint4((uint32_t)asz0, 0, 0, 0);
+  // Head records read here: a crossing book's, all where the call hands out the
+  // BBO, and a head whose size the cache does not hold (so that this call's
+  // epilogue caches it and get_bbos, every step until the head changes, reads
+  // no record for it).
   const bool head_recs = cross || (kSizes && !carried);
-  if (head_recs && !bid_top && hb0 < (uint32_t)O) hrb = rec[hb0];
-  if (head_recs && !ask_top && ha0 < (uint32_t)O) hra = rec[ha0];
+  const bool load_b = !bid_top && hb0 < (uint32_t)O && (head_recs || !(hb0f & kSizeKnown));
+  const bool load_a = !ask_top && ha0 < (uint32_t)O && (head_recs || !(ha0f & kSizeKnown));
+  if (load_b) hrb = rec[hb0];
+  if (load_a) hra = rec[ha0];
   int pb = -1, pa = L;
   uint32_t pbh = kNull16, pah = kNull16;
   if (cross) {
@@ -1132,13 +1138,12 @@ ASTRA_HD void quote_prologue(const Book &b, const QuoteIn &in, int64_t m, Market
     s.ah = ask_top ? aslot : ha0;
     s.arec = patched(s.ah, hra);
   }
-  // The head records in registers: read above (a crossing book, or where the
-  // call hands out the BBO itself, or carried), or written by this call's
-  // inserts. A head the call does not touch and whose record it did not read
-  // keeps the size cached by an earlier call, if that call cached it.
-  const bool sizes_in = head_recs || (kSizes && carried);
-  s.have_b = bb >= 0 && (sizes_in || s.bh == bslot || s.bh == aslot);
-  s.have_a = ba < L && (sizes_in || s.ah == bslot || s.ah == aslot);
+  // The head records in registers: read above, carried, or written by this
+  // call's inserts. A head the call does not touch and whose record it did not
+  // read keeps the size cached by an earlier call.
+  const bool sizes_in = kSizes && carried;
+  s.have_b = bb >= 0 && (sizes_in || bid_top || load_b || s.bh == bslot || s.bh == aslot);
+  s.have_a = ba < L && (sizes_in || ask_top || load_a || s.ah == bslot || s.ah == aslot);
   c.keep_b = !cross && !s.have_b && bb >= 0 && !bid_top && hb0f != kNull16 && (hb0f & kSizeKnown) &&
              hb0 != 0x7FFFu;
   c.keep_a = !cross && !s.have_a && ba < L && !ask_top && ha0f != kNull16 && (ha0f & kSizeKnown) &&
@@ -1650,6 +1655,7 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
     add_u64(b.stats + 7, (unsigned long long)(s.npass > 0 ? 1 : 0));
     add_u64(b.stats + 8, (unsigned long long)s.zruns);
     add_u64(b.stats + 9, (unsigned long long)s.zrows);
+    add_u64(b.stats + 10, (unsigned long long)((bv && !wb && !c.keep_b) + (av && !wa && !c.keep_a)));
   }
 }
 

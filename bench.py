@@ -325,7 +325,7 @@ def bench_market(args, cfg_index: int, secondary: bool = False, markets: int = 0
             bbo_ms = ev[1].elapsed_time(ev[2]) / K
 
     # ---- D: exact work counts for the algorithmic bytes ----
-    counters = torch.zeros(10, dtype=torch.int64, device=dev)
+    counters = torch.zeros(11, dtype=torch.int64, device=dev)
     if "D" in phases:
         snaps["D"]._set_stats(counters)
         for t in range(T0, T):
@@ -333,7 +333,7 @@ def bench_market(args, cfg_index: int, secondary: bool = False, markets: int = 0
         torch.cuda.synchronize()
         snaps["D"]._set_stats(None)
     (n_ins, n_fill, n_empty, n_ovf, n_ff, n_pass, n_staged, n_cross, n_zruns,
-     n_zrows) = (int(x) for x in counters.cpu().tolist())
+     n_zrows, n_bbo_book) = (int(x) for x in counters.cpu().tolist())
 
     # ---- R: the same steps with the row layout of the FillBatch ----
     wall_rows = None
@@ -459,6 +459,7 @@ def bench_market(args, cfg_index: int, secondary: bool = False, markets: int = 0
                           "overflow_markets": n_ovf / K, "crossing_markets": n_cross / K,
                           "loop_passes": n_pass / K, "staged_markets": n_staged / K,
                           "staged_zero_runs": n_zruns / K, "staged_zero_rows": n_zrows / K,
+                          "bbo_sides_read_from_book": n_bbo_book / K,
                           "staged_counts_note": "staged_* come from the counting kernel, which "
                                                 "stages serially (no helper wavefronts); the other "
                                                 "counts are the work of any launch shape"},
@@ -529,7 +530,7 @@ def bench_sweep(args):
             step(q)
         torch.cuda.synchronize()
         wall = time.perf_counter() - a0
-        counters = torch.zeros(10, dtype=torch.int64, device=dev)
+        counters = torch.zeros(11, dtype=torch.int64, device=dev)
         market._set_stats(counters)
         for q in window[K:2 * K]:
             market.add_two_sided_quotes(*q, fills)
@@ -640,7 +641,7 @@ def bench_game(args, secondary: bool = False):
     # D: work counts of the matching kernel
     st = snaps[3]
     st.set_check_moves(False)
-    counters = torch.zeros(10, dtype=torch.int64, device=dev)
+    counters = torch.zeros(11, dtype=torch.int64, device=dev)
     st.market._set_stats(counters)
     for k in range(T0, T0 + K):
         st.apply_action(moves[k])

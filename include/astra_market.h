@@ -179,14 +179,16 @@ int astra_market_shape(const astra_market *market, int32_t *num_markets, int32_t
 int astra_market_to_string(const astra_market *market, int32_t market_id, char *buf,
                            size_t buflen, size_t *needed, void *stream);
 
-/* Diagnostic, no counterpart in the reference: while `counters` (int64 [10],
+/* Diagnostic, no counterpart in the reference: while `counters` (int64 [11],
  * device memory, caller-zeroed) is set, astra_market_add_two_sided_quotes also
- * adds to [0..9] the accepted order inserts, fill rows written (F for a market
+ * adds to [0..10] the accepted order inserts, fill rows written (F for a market
  * that overflowed), price levels emptied, markets that overflowed, overflows
  * reached by fast-forwarding a repeating loop state, matching-loop passes,
  * markets finished from a staged (LDS) copy of their book, markets whose
  * book crossed (that entered the matching loop), runs of zero-size fill rows
- * listed on a staged book, and the rows of those runs.
+ * listed on a staged book, the rows of those runs, and the best levels whose
+ * head size the call left uncached (which astra_market_get_bbos then reads
+ * from the book's order records).
  * These are the work counts of the algorithmic-byte roofline. NULL switches it
  * off (the default); the timed path never has it on. */
 int astra_market_set_stats(astra_market *market, int64_t *counters);

@@ -63,7 +63,7 @@ def _run(M, L, O, F, C, steps, gen, with_stats=False, stage_budget=None, layout=
     em, om = _emu(M, L, O, F, C, stage_budget, extended, fill_rows), OracleMarket(M, L, O, F, C)
     ef, of = em.new_fill_batch(layout), om.new_fill_batch()
     eb, ob = em.new_bbo_batch(), om.new_bbo_batch()
-    stats = np.zeros(10, np.int64)
+    stats = np.zeros(11, np.int64)
     ostats = {"inserts": 0, "fills": 0, "levels_emptied": 0, "overflows": 0}
     if with_stats:
         em.set_stats(stats)
@@ -86,6 +86,8 @@ def _run(M, L, O, F, C, steps, gen, with_stats=False, stage_budget=None, layout=
         ostats["staged"] = int(stats[6])
         ostats["zero_runs"] = int(stats[8])
         ostats["zero_rows"] = int(stats[9])
+        ostats["crossing"] = int(stats[7])
+        ostats["bbo_book_reads"] = int(stats[10])
     assert em.global_tid == om.global_tid
     ostats["last_fills"] = of
     return em, om, ostats
@@ -155,8 +157,14 @@ def test_emulated_config3_and_4_samples(stage_budget, layout, fill_rows):
     for idx, M, steps in ((3, 300, 700), (4, 60, 400)):
         cfg = CONFIGS[idx]
         qs = QuoteStream(cfg, np.arange(M))
-        _run(M, cfg.L, cfg.O, cfg.F, cfg.C, steps, qs.step, with_stats=True, stage_budget=stage_budget,
-             layout=layout, fill_rows=fill_rows)
+        _, _, st = _run(M, cfg.L, cfg.O, cfg.F, cfg.C, steps, qs.step, with_stats=True,
+                        stage_budget=stage_budget, layout=layout, fill_rows=fill_rows)
+        # A best level's head size is left for get_bbos to read from the book
+        # only where the call's matching loop moved that side to a head whose
+        # record it did not read (the next call reads and caches it): at most
+        # two sides per crossing market, and far fewer than the 2 M per step a
+        # cache that never refills would leave.
+        assert 0 < st["bbo_book_reads"] <= 2 * st["crossing"], (idx, st)
 
 
 def test_emulated_reset_clear_clone_to_string():
