@@ -65,6 +65,26 @@ def log(msg: str) -> None:
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
+class HostInputs:
+    """The host generator's steps (QuoteStream, numpy), uploaded one by one: the
+    same int32 inputs as DeviceQuoteStream, with no generator kernels on the GPU."""
+
+    def __init__(self, cfg, markets, dev):
+        from astra_cuda.workloads import QuoteStream
+        self.qs, self.dev = QuoteStream(cfg, markets), dev
+
+    def step(self, t):
+        import numpy as np
+        import torch
+        return tuple(torch.from_numpy(np.ascontiguousarray(x, dtype=np.int32)).to(self.dev)
+                     for x in self.qs.step(t))
+
+    def steps(self, t0, t1):
+        import torch
+        rows = [self.step(t) for t in range(t0, t1)]
+        return tuple(torch.stack([r[i] for r in rows]) for i in range(5))
+
+
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -97,6 +117,10 @@ def parse_args():
     ap.add_argument("--scatter-calibration", action="store_true",
                     help="only time scattered 4-byte writes, reads and atomic adds into a 1 GiB "
                          "buffer (the rate of scattered memory requests the device sustains)")
+    ap.add_argument("--host-inputs", action="store_true",
+                    help="generate the quotes with the host generator (numpy; the same values as the "
+                         "device generator) and upload them step by step: for profiler runs that "
+                         "should see no generator kernels")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for rocprof counter scaling)")
     return ap.parse_args()
@@ -233,7 +257,10 @@ def bench_market(args, cfg_index: int, secondary: bool = False, markets: int = 0
     # warm-up on are generated up front and resident in HBM before timing, the
     # pre-roll's step by step ----
     t0 = time.perf_counter()
-    dq = DeviceQuoteStream(cfg, None if M == cfg.M else np.arange(M), device=dev)
+    if args.host_inputs:
+        dq = HostInputs(cfg, np.arange(M), dev)
+    else:
+        dq = DeviceQuoteStream(cfg, None if M == cfg.M else np.arange(M), device=dev)
     shape = dict(num_markets=M, max_price_levels=cfg.L, max_active_orders_per_market=cfg.O,
                  max_active_fills_per_market=cfg.F, num_customers=cfg.C)
     market = aom.VecMarket(**shape, allow_extended_shapes=cfg.extended)
@@ -252,7 +279,8 @@ def bench_market(args, cfg_index: int, secondary: bool = False, markets: int = 0
     for t in range(S, T0):
         step(market, rows[t])
     torch.cuda.synchronize()
-    log(f"config {cfg.index}: {M} markets, pre-roll ({S} steps, inputs generated on the device) and "
+    where = "on the host" if args.host_inputs else "on the device"
+    log(f"config {cfg.index}: {M} markets, pre-roll ({S} steps, inputs generated {where}) and "
         f"warm-up ({W} steps) in {time.perf_counter() - t0:.1f}s; timing steps [{T0}, {T})")
     # state at the start of the timed steps, for the replays B, C, D, R, S and G
     snaps = {p: market.clone() for p in "BCDRSG" if p in phases}
