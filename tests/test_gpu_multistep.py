@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle.oracle import OracleMarket
-from parity_util import DEV, make_market, t32
+from parity_util import DEV, compare_fills, make_market, t32
 from ws_layout import normalized
 
 pytestmark = pytest.mark.gpu
@@ -71,6 +71,8 @@ def _run(M, L, O, F, C, stream, warm, chunks, layout, stage_budget=None, oracle=
             assert torch.equal(getattr(fm, f), getattr(fs, f)), (t, f)
         if om is not None:
             assert np.array_equal(multi.get_customer_portfolios().cpu().numpy(), om.customer_portfolios)
+            if K:  # the last step's rows, field by field
+                compare_fills(fm, fo, F, f"multi-step launch ending at step {t}")
     bm = multi.new_bbo_batch()
     multi.get_bbos(bm)  # the BBO cache a later get_bbos reads is the last step's
     for f in BBO:
@@ -124,3 +126,27 @@ def test_gpu_multistep_configs(idx, M, warm, chunks, layout):
         return cache[t]
 
     _run(M, cfg.L, cfg.O, cfg.F, cfg.C, stream, warm, chunks, layout)
+
+
+@pytest.mark.parametrize("idx,M,warm,chunks,layout,knobs", [
+    (3, 4000, 500, [20, 1, 39], "columns", {}),          # past the ring wrap (step 512)
+    (3, 4000, 500, [60], "rows", {"per_wave": 16}),
+    (2, 3000, 2000, [20, 20], "columns", {}),            # the ring wrapped about 4 times
+    (4, 1500, 300, [25, 25], "columns", {}),             # W = 8, extended shape
+])
+def test_gpu_multistep_configs_vs_oracle(idx, M, warm, chunks, layout, knobs):
+    """Launches of several steps at the config shapes, with thousands of markets and
+    after the order ring has wrapped, against the oracle step by step (fill counts
+    and BBOs of every step, the last step's rows, portfolios), besides the single
+    calls."""
+    from astra_cuda.workloads import CONFIGS, QuoteStream
+    cfg = CONFIGS[idx]
+    qs = QuoteStream(cfg, np.arange(M))
+    cache = {}
+
+    def stream(t):
+        if t not in cache:
+            cache[t] = qs.step(t)
+        return cache[t]
+
+    _run(M, cfg.L, cfg.O, cfg.F, cfg.C, stream, warm, chunks, layout, oracle=True, **knobs)
