@@ -92,9 +92,23 @@ ASTRA_HD void observation_element(const astra_hl_observation &o, int64_t i) {
   o.values[i] = v;
 }
 
-__global__ __launch_bounds__(kBlock) void trade_check_kernel(GameMove g, int64_t N) {
+// The checks of every env OR-ed into g.errors. With `errors_host` (pinned host
+// memory, zeroed by the host before the launch), a workgroup with a failed
+// check also stores its bits there, so that the host learns whether any check
+// failed without a copy on the stream; it reads the exact bits from g.errors
+// only then.
+__global__ __launch_bounds__(kBlock) void trade_check_kernel(GameMove g, int64_t N, int32_t *errors_host) {
+  __shared__ int32_t acc;
   const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (n < N) trade_check(g, n);
+  if (threadIdx.x == 0) acc = 0;
+  __syncthreads();
+  const int32_t bad = n < N ? game_quote(g, n).bad : 0;
+  if (bad) atomicOr(&acc, bad);
+  __syncthreads();
+  if (threadIdx.x == 0 && acc) {
+    atomicOr(g.errors, acc);
+    if (errors_host) __hip_atomic_store(errors_host, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 __global__ __launch_bounds__(kBlock) void observation_kernel(astra_hl_observation o, int64_t total) {
@@ -269,13 +283,19 @@ __global__ __launch_bounds__(kBlock) void rewards_kernel(const int32_t *src, flo
 
 inline unsigned grid_for(int64_t n) { return (unsigned)((n + kBlock - 1) / kBlock); }
 
-int launch_check(const GameMove &g, int64_t N, hipStream_t s) {
+// errors_host: see trade_check_kernel (the host zeroes it here, before the launch;
+// no earlier launch that may store to it is still running, since the host waited
+// for the last check).
+int launch_check(const GameMove &g, int64_t N, int32_t *errors_host, hipStream_t s) {
+  if (errors_host) *errors_host = 0;
 #ifdef ASTRA_HOST_EMULATION
   (void)s;
   for (int64_t n = 0; n < N; ++n) trade_check(g, n);
+  if (errors_host) *errors_host = *g.errors;
   return ASTRA_OK;
 #else
-  if (N > 0) hipLaunchKernelGGL(trade_check_kernel, dim3(grid_for(N)), dim3(kBlock), 0, s, g, N);
+  if (N > 0)
+    hipLaunchKernelGGL(trade_check_kernel, dim3(grid_for(N)), dim3(kBlock), 0, s, g, N, errors_host);
   ASTRA_HIP_CHECK(rt_last_error(), "trade_check_kernel launch");
   return ASTRA_OK;
 #endif
@@ -428,11 +448,9 @@ int trade_impl(astra_market *market, const astra_hl_trade *t, int32_t *errors, h
   StreamMark checked;
   checked.ev = ev;
   if (t->check) {
-    if ((rc = launch_check(g, M, s))) return rc;
-    if (t->errors_host) {
-      ASTRA_HIP_CHECK(rt_memcpy(t->errors_host, errors, sizeof(int32_t), s), "error flags copy");
-      ASTRA_HIP_CHECK(checked.record(s), "error flags event");
-    }
+    // (with errors_host a failed check's workgroup marks it there itself)
+    if ((rc = launch_check(g, M, t->errors_host, s))) return rc;
+    if (t->errors_host) ASTRA_HIP_CHECK(checked.record(s), "error flags event");
   }
   // the move itself: one launch of the matching kernel with the game's work fused
   if ((rc = astra_game_move(market, g, fields, t->fill_rows, t->fill_counts, s))) return rc;
@@ -440,6 +458,10 @@ int trade_impl(astra_market *market, const astra_hl_trade *t, int32_t *errors, h
   if (t->errors_host) {
     ASTRA_HIP_CHECK(checked.wait(), "error flags wait");
     bits = *t->errors_host;
+    if (bits) {  // a check failed: all of them, from the device word (the checks are done)
+      ASTRA_HIP_CHECK(rt_memcpy(&bits, errors, sizeof(bits), s), "error flags copy");
+      ASTRA_HIP_CHECK(rt_sync(s), "error flags wait");
+    }
   } else {
     ASTRA_HIP_CHECK(rt_memcpy(&bits, errors, sizeof(bits), s), "error flags copy");
     ASTRA_HIP_CHECK(rt_sync(s), "error flags wait");
