@@ -1606,16 +1606,30 @@ ASTRA_HD void quote_epilogue(const Book &b, const FillOut &out, const MarketCtx 
   // only for the others.
   // (slot 0x7FFF, possible at O = 32768, is never flagged: flagged it would read
   // as NULL)
-  const bool wb = bv && (kSizes || s.have_b) && s.bh != 0x7FFFu;
-  const bool wa = av && (kSizes || s.have_a) && s.ah != 0x7FFFu;
+  // (on a staged book a head's record is an LDS read away: every head's size is
+  // cached there)
+  bool hb = s.have_b, ha = s.have_a;
+  int32_t bsz_c = (int32_t)s.brec.x, asz_c = (int32_t)s.arec.x;
+  if constexpr (BookMem::kStaged && !kSizes) {
+    if (!hb && bv) {
+      bsz_c = bk.size(s.bh);
+      hb = true;
+    }
+    if (!ha && av) {
+      asz_c = bk.size(s.ah);
+      ha = true;
+    }
+  }
+  const bool wb = bv && (kSizes || hb) && s.bh != 0x7FFFu;
+  const bool wa = av && (kSizes || ha) && s.ah != 0x7FFFu;
   const uint32_t tob = (bv ? (s.bh | ((wb || c.keep_b) ? kSizeKnown : 0u)) : kNull16) |
                        ((av ? (s.ah | ((wa || c.keep_a) ? kSizeKnown : 0u)) : kNull16) << 16);
   if (store) {
     b.bbo[m] = obp;
     b.bbo[M + m] = oap;
     b.tob[m] = tob;
-    if (wb) b.hsz[m] = kSizes ? obs : (int32_t)s.brec.x;
-    if (wa) b.hsz[M + m] = kSizes ? oas : (int32_t)s.arec.x;
+    if (wb) b.hsz[m] = kSizes ? obs : bsz_c;
+    if (wa) b.hsz[M + m] = kSizes ? oas : asz_c;
   }
   if (MULTI && Carry<W>::kState && cy) {
 #pragma unroll
@@ -2103,9 +2117,24 @@ __global__ __launch_bounds__(256) void quote_match_kernel(Book b, QuoteIn in, Fi
         if (match_loop<W, STATS, false>(st, c, gb, sink, out, bulk, 0x7FFFFFFF, &hand))
           quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, gb, ink.game, sok, &cy, last);
       } else if (match_loop<W, STATS, !GAME>(st, c, gb, sink, out, bulk, budget)) {
-        if constexpr (kApart)
+        if constexpr (kApart) {
           finished = true;
-        else
+          // The records of heads the loop moved to without reading them, loaded
+          // now so that the epilogue after the staged walks caches their sizes
+          // (get_bbos then reads no record for this market): the loads complete
+          // while the wavefront stages its walks, off its critical path.
+          if (!GAME && !MULTI) {
+            const uint32_t O = (uint32_t)c.O;
+            if (!st.have_b && st.bb >= 0 && st.bh < O && st.bh != 0x7FFFu) {
+              st.brec = gb.record(st.bh);
+              st.have_b = true;
+            }
+            if (!st.have_a && st.ba < c.L && st.ah < O && st.ah != 0x7FFFu) {
+              st.arec = gb.record(st.ah);
+              st.have_a = true;
+            }
+          }
+        } else
           quote_epilogue<W, STATS, GAME, MULTI>(b, out, c, st, sink, gb, ink.game, sok, &cy, last);
       } else {
         sink.flush(out, c.pf, c.C);  // the staged walk's rows follow these
