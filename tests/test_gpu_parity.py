@@ -59,6 +59,20 @@ def test_gpu_config2_subset():
     assert r["fill_rows"] > 3000
 
 
+@pytest.mark.parametrize("stage_budget", [None, 1])
+def test_gpu_config2_subset_after_many_wraps(stage_budget):
+    """Config 2 markets 0..1999 for 3000 steps: the ring of 1024 orders wraps about
+    six times, so crossing quotes walk chains of consumed orders (zero-size fills,
+    levels emptied one after another) on the staged book's lean runs; with stage
+    budget 1 every market that crosses twice in a call is finished staged. Every
+    row of every step is compared with the oracle."""
+    cfg, gen = _stream_gen(2, np.arange(2000))
+    _log(f"config 2 subset: 2000 x 3000, stage budget {stage_budget}")
+    r = run_parity(2000, cfg.L, cfg.O, cfg.F, cfg.C, 3000, gen, full_every=500, label="cfg2 wraps",
+                   stage_budget=stage_budget)
+    assert r["fill_rows"] > 2000
+
+
 @pytest.mark.parametrize("stage_budget,layout", [(None, "columns"), (1, "columns"), (None, "rows")])
 def test_gpu_config3_subset_with_eviction(stage_budget, layout):
     """Config 3 markets 0..3999 for all 1000 steps (the ring of 1024 wraps after 512 steps).
