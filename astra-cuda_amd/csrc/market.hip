@@ -345,10 +345,28 @@ struct Bulk {
 // longer knows they point to global memory; plain stores through them become
 // flat stores, which also count against the LDS/scalar counter, so every later
 // wait for an LDS access would wait for those stores to reach memory too.
+// HIP's vector types assign through a member operator, whose `this` is a
+// generic pointer, so their lanes go out as a native vector (2 or 4 lanes) or
+// as three 4-byte stores (which the compiler merges into one 12-byte store;
+// a 3-lane native vector would be stored as 4 lanes, one too many).
 template <class T>
 ASTRA_HD void gst(T *p, const T &v) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  *(__attribute__((address_space(1))) T *)p = v;
+  if constexpr (std::is_same_v<T, int4> || std::is_same_v<T, uint4>) {
+    typedef int32_t v4 __attribute__((ext_vector_type(4)));
+    *(__attribute__((address_space(1))) v4 *)p =
+        v4{(int32_t)v.x, (int32_t)v.y, (int32_t)v.z, (int32_t)v.w};
+  } else if constexpr (std::is_same_v<T, int2> || std::is_same_v<T, uint2>) {
+    typedef int32_t v2 __attribute__((ext_vector_type(2)));
+    *(__attribute__((address_space(1))) v2 *)p = v2{(int32_t)v.x, (int32_t)v.y};
+  } else if constexpr (std::is_same_v<T, int3>) {
+    __attribute__((address_space(1))) int32_t *q = (__attribute__((address_space(1))) int32_t *)p;
+    q[0] = v.x;
+    q[1] = v.y;
+    q[2] = v.z;
+  } else {
+    *(__attribute__((address_space(1))) T *)p = v;
+  }
 #else
   *p = v;
 #endif
