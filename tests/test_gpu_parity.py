@@ -36,10 +36,10 @@ def test_gpu_library_is_the_in_tree_build():
     assert lib._name.endswith("astra_cuda/libastra_market.so")
 
 
-def _stream_gen(cfg_index, markets=None, M_override=None):
+def _stream_gen(cfg_index, markets=None, M_override=None, seed=0):
     from astra_cuda.workloads import CONFIGS, QuoteStream
     cfg = CONFIGS[cfg_index]
-    qs = QuoteStream(cfg, markets)
+    qs = QuoteStream(cfg, markets, seed=seed)
     return cfg, qs.step
 
 
@@ -71,6 +71,19 @@ def test_gpu_config2_subset_after_many_wraps(stage_budget):
     r = run_parity(2000, cfg.L, cfg.O, cfg.F, cfg.C, 3000, gen, full_every=500, label="cfg2 wraps",
                    stage_budget=stage_budget)
     assert r["fill_rows"] > 2000
+
+
+@pytest.mark.parametrize("cfg_index,M,steps,seed", [
+    (3, 3000, 1000, 7), (3, 3000, 1000, 201), (2, 1500, 3000, 13), (4, 300, 2000, 99)])
+def test_gpu_streams_with_other_seeds(cfg_index, M, steps, seed):
+    """The config streams drawn with seeds other than their own (0): other books,
+    other crossings and, after the ring wraps, other chains of consumed orders,
+    every row of every step against the oracle."""
+    cfg, gen = _stream_gen(cfg_index, np.arange(M), seed=seed)
+    _log(f"config {cfg_index} stream, seed {seed}: {M} x {steps}")
+    r = run_parity(M, cfg.L, cfg.O, cfg.F, cfg.C, steps, gen, full_every=250,
+                   label=f"cfg{cfg_index} seed {seed}")
+    assert r["fill_rows"] > M
 
 
 @pytest.mark.parametrize("stage_budget,layout", [(None, "columns"), (1, "columns"), (None, "rows")])
