@@ -30,6 +30,11 @@ namespace {
 
 constexpr int kBlock = 256;
 
+// The observation and reward tensors are written once per call and read later by
+// the caller, never by these kernels: non-temporal stores stream them past the
+// caches (the observation of 262,144 envs, 44 MB, by about 2.5 us per call).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 static_assert(ASTRA_HL_ERR_BID_PRICE_LOW == 1 && ASTRA_HL_ERR_ASK_PRICE_LOW == 2 &&
                   ASTRA_HL_ERR_BID_PRICE_HIGH == 4 && ASTRA_HL_ERR_ASK_PRICE_HIGH == 8 &&
                   ASTRA_HL_ERR_BID_SIZE_LOW == 16 && ASTRA_HL_ERR_ASK_SIZE_LOW == 32 &&
@@ -240,12 +245,12 @@ __global__ __launch_bounds__(kObsTileWaves * 64) void observation_tile_kernel(as
         const int32_t e = (f + q) / D, jj = (f + q) - e * D;
         v[q] = tile[e * pitch + jj];
       }
-      *reinterpret_cast<float4 *>(dst + f) = make_float4(v[0], v[1], v[2], v[3]);
+      __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4 *>(dst + f));
     }
   } else {
     for (int32_t f = lane; f < total; f += 64) {
       const int32_t e = f / D, jj = f - e * D;
-      dst[f] = tile[e * pitch + jj];
+      __builtin_nontemporal_store(tile[e * pitch + jj], dst + f);
     }
   }
 }
@@ -267,17 +272,18 @@ __global__ __launch_bounds__(kBlock) void rewards_kernel(const int32_t *src, flo
                                                          int32_t stride, int32_t col, int32_t vec) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (col >= 0) {
-    if (i < n) dst[i] = (float)src[i * stride + col];
+    if (i < n) __builtin_nontemporal_store((float)src[i * stride + col], dst + i);
   } else if (vec) {
     const int64_t k = i * 4;
     if (k + 4 <= n) {
       const int4 v = *reinterpret_cast<const int4 *>(src + k);
-      *reinterpret_cast<float4 *>(dst + k) = make_float4((float)v.x, (float)v.y, (float)v.z, (float)v.w);
+      __builtin_nontemporal_store(f32x4{(float)v.x, (float)v.y, (float)v.z, (float)v.w},
+                                  reinterpret_cast<f32x4 *>(dst + k));
     } else {
-      for (int64_t q = k; q < n; ++q) dst[q] = (float)src[q];
+      for (int64_t q = k; q < n; ++q) __builtin_nontemporal_store((float)src[q], dst + q);
     }
   } else if (i < n) {
-    dst[i] = (float)src[i];
+    __builtin_nontemporal_store((float)src[i], dst + i);
   }
 }
 
