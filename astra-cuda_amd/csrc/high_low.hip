@@ -32,7 +32,9 @@ constexpr int kBlock = 256;
 
 // The observation and reward tensors are written once per call and read later by
 // the caller, never by these kernels: non-temporal stores stream them past the
-// caches (the observation of 262,144 envs, 44 MB, by about 2.5 us per call).
+// caches, which keep the move's books (the observation of 262,144 envs, 44 MB:
+// the game step about 3% faster). The observation's column loads, each word read
+// once per call, are non-temporal too.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 static_assert(ASTRA_HL_ERR_BID_PRICE_LOW == 1 && ASTRA_HL_ERR_ASK_PRICE_LOW == 2 &&
@@ -224,7 +226,7 @@ __global__ __launch_bounds__(kObsTileWaves * 64) void observation_tile_kernel(as
 #pragma unroll
   for (int32_t j = 7; j < D; ++j) {
     const ObsColumn c = obs_column(o, j);
-    word[j] = c.src[n * c.stride];
+    word[j] = __builtin_nontemporal_load(c.src + n * c.stride);  // read once per call
   }
   float *tile = obs_tile + w * 64 * pitch;
 #pragma unroll
